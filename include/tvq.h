@@ -1,0 +1,124 @@
+/*
+ * tvq.h — C ABI of the MI355X (gfx950) quantized-linear library
+ * (libtinyvllm_quant.so).
+ *
+ * This library is the device half of tiny-vLLM's quantized Linear hot path:
+ * the INT8 weight-only GEMM (W8A16) and the W8A8 GEMM with per-token dynamic
+ * activation quantization. Every entry point takes plain device pointers,
+ * sizes and a hipStream_t passed as `void*`. The library never allocates,
+ * never synchronises the stream and launches only on the stream it is given,
+ * so every call is safe inside HIP-graph capture. All buffers (outputs
+ * included) are owned by the caller.
+ *
+ * Layouts (all row-major, contiguous, leading dimension = number of columns):
+ *   x        [M, K]  bf16 or fp16 activations
+ *   xq       [M, K]  int8 quantized activations
+ *   a_scales [M]     fp32 per-token activation scales
+ *   qweight  [N, K]  int8 weights, the on-disk `*.qweight` layout unchanged
+ *   scales   [N]     fp32 per-output-channel weight scales (`*.scales` /
+ *                    `*.w_scales` on disk)
+ *   bias     [N]     same dtype as the output, or NULL
+ *   y        [M, N]  bf16 or fp16 output (int32 for tvq_w8a8_gemm_i32)
+ *
+ * Return codes: TVQ_OK (0) on success, a negative TVQ_E* code otherwise;
+ * tvq_last_error() then describes the failure (thread-local string).
+ */
+#ifndef TVQ_H_
+#define TVQ_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TVQ_ABI_VERSION 1
+
+/* Activation / output element types. */
+enum tvq_dtype {
+  TVQ_DTYPE_F16 = 0,
+  TVQ_DTYPE_BF16 = 1,
+};
+
+/* Operation ids for tvq_select_path. */
+enum tvq_op {
+  TVQ_OP_ACT_QUANT = 0,
+  TVQ_OP_W8A16 = 1,
+  TVQ_OP_W8A8 = 2,
+};
+
+enum tvq_status {
+  TVQ_OK = 0,
+  TVQ_E_INVALID = -1,     /* bad pointer, size or dtype */
+  TVQ_E_UNSUPPORTED = -2, /* shape/alignment the library cannot run */
+  TVQ_E_HIP = -3,         /* a HIP runtime call failed (launch error) */
+};
+
+/* Version of this ABI (TVQ_ABI_VERSION). No reference counterpart: the
+ * reference's pybind11 modules are versioned by their JIT build hash. */
+int tvq_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). Replaces the
+ * TORCH_CHECK messages of int8_weight_only_gemm.cpp:19-36 and w8a8_gemm.cpp. */
+const char* tvq_last_error(void);
+
+/* Name of the kernel path the library would pick for this op and shape.
+ * Replaces `select_path(x, qweight)` of the reference's extensions
+ * (int8_weight_only_gemm.cpp:42, int8_weight_only_gemm.cu:545-547;
+ * w8a8_gemm.cpp, w8a8_gemm.cu:405-411). `dtype` is the activation dtype for
+ * W8A16 / ACT_QUANT and the output dtype for W8A8. The returned string is
+ * static. Returns NULL for an invalid op. */
+const char* tvq_select_path(int op, int64_t M, int64_t N, int64_t K, int dtype);
+
+/* Per-token (per-row) dynamic symmetric int8 quantization of x [M, K]:
+ *   s[m]    = max(amax_k |x[m,k]| / 127, eps)           (fp32, IEEE RN)
+ *   xq[m,k] = clamp(rint_half_even(x[m,k] / s[m]), -127, 127)
+ * Bit-exact restatement of quantize_int8_per_row_dynamic
+ * (nanovllm/quantization/utils.py:28-32) as called by
+ * W8A8QuantMethod.quantize_activation (nanovllm/quantization/w8a8.py:21-23).
+ * The reference runs this as ~9 torch kernels; here it is one pass. */
+int tvq_act_quant(const void* x, int dtype, int64_t M, int64_t K, float eps,
+                  int8_t* xq, float* a_scales, void* stream);
+
+/* W8A16: y = x · (qweight · diag(scales))^T + bias, fp32 accumulation, the
+ * per-channel fp32 scale applied once per output. Replaces the extension
+ * `forward(x, qweight, scales, bias)` (int8_weight_only_gemm.cpp:14-37,
+ * int8_weight_only_gemm.cu:549-618) behind native_int8_weight_only_linear
+ * (nanovllm/quantization/cuda.py:261-274). */
+int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight,
+                   const float* scales, const void* bias, void* y, int64_t M,
+                   int64_t N, int64_t K, void* stream);
+
+/* W8A8: acc[m,n] = sum_k xq[m,k]·qweight[n,k] (exact int32),
+ *   y[m,n] = out((float(acc)·a_scales[m])·w_scales[n] + bias[n]).
+ * Replaces the extension `forward(x_q, a_scales, qweight, w_scales, bias,
+ * use_bfloat16)` (w8a8_gemm.cpp:16-54, w8a8_gemm.cu:426-507) behind
+ * native_w8a8_linear (nanovllm/quantization/cuda.py:435-452). `out_dtype`
+ * selects bf16 (use_bfloat16=True) or fp16 output. */
+int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales,
+                  const int8_t* qweight, const float* w_scales,
+                  const void* bias, void* y, int out_dtype, int64_t M,
+                  int64_t N, int64_t K, void* stream);
+
+/* The raw exact int32 accumulator acc[m,n] = sum_k xq[m,k]·qweight[n,k] of
+ * the W8A8 path, written to y_i32 [M, N], using the same kernel selection as
+ * tvq_w8a8_gemm. No reference counterpart as an entry point: it exposes the
+ * accumulator the reference forms inside w8a8_gemm_wmma_kernel
+ * (w8a8_gemm.cu:336-375) so it can be checked bit-exactly. */
+int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32,
+                      int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Fused W8A8 linear: tvq_act_quant(x) into the caller's xq / a_scales buffers
+ * followed by tvq_w8a8_gemm, both on `stream`. Replaces the pair
+ * W8A8QuantMethod.quantize_activation + apply_w8a8_linear inside
+ * W8A8QuantMethod.apply (nanovllm/quantization/w8a8.py:25-40). */
+int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight,
+                    const float* w_scales, const void* bias, void* y,
+                    int64_t M, int64_t N, int64_t K, int8_t* xq_buf,
+                    float* a_scales_buf, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TVQ_H_ */

@@ -1,0 +1,34 @@
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG = ROOT / "tiny-vllm_amd"
+for p in (str(ROOT), str(PKG)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X); run with -m gpu")
+
+
+@pytest.fixture(scope="session")
+def hiplib():
+    """The built C-ABI library (built on demand if absent)."""
+    from nanovllm.quantization import _hip
+    if not _hip.library_path().is_file():
+        sys.path.insert(0, str(PKG))
+        import build as tvq_build
+        tvq_build.build()
+    return _hip.load_library()
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a visible ROCm device")
+    return torch.device("cuda", 0)

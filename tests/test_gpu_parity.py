@@ -1,0 +1,259 @@
+"""GPU parity tests: the HIP kernels (through the C ABI) against the oracle.
+
+Bar:
+  * act-quant int8 values and fp32 scales: bit-exact;
+  * W8A8 int32 accumulators: bit-exact;
+  * W8A8 bf16/fp16 outputs: bit-exact against the oracle's restatement of the
+    reference kernel's epilogue, and within rel-L2 <= 1e-2,
+    max-abs <= 2e-2*max|ref| of the reference's torch path;
+  * W8A16 outputs: within the same tolerance of the torch path and within a
+    bf16-rounding bound of the exact fp64 product.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import bits16, f32, make_activations, make_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    return torch.device("cuda", 0)
+
+
+def _log_case(**kw):
+    print("CASE", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+# ---------------------------------------------------------------- act quant
+
+ACT_SHAPES = [(1, 1024), (3, 1024), (64, 1024), (257, 3072), (33, 4096), (5, 12288), (2, 8), (7, 24), (9, 100),
+              (1, 1)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", ACT_SHAPES)
+def test_act_quant_bit_exact(hiplib, shape, dtype):
+    from nanovllm.quantization import _hip
+    m, k = shape
+    _log_case(test="act_quant", m=m, k=k, dtype=dtype)
+    x = make_activations(m, k, seed=m * 131 + k, dtype=dtype)
+    if m >= 3:
+        x[1].zero_()                       # all-zero row -> s = eps, q = 0
+        x[2] = x[2] * 1e-30 if dtype == torch.bfloat16 else x[2] * 1e-6  # tiny/subnormal row
+    q_ref, s_ref = oracle.c_act_quant(bits16(x), is_bf16=dtype == torch.bfloat16)
+    xq, s = _hip.act_quant(x.to(_dev()))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(xq.cpu().numpy(), q_ref)
+    # and against the reference's own torch expression on the CPU
+    q_t, s_t = oracle.quantize_rows_torch(x)
+    np.testing.assert_array_equal(xq.cpu().numpy(), q_t.numpy())
+
+
+def test_act_quant_ties_half_even(hiplib):
+    """x/s lands exactly on k+0.5: must round to even (torch.round semantics)."""
+    from nanovllm.quantization import _hip
+    # amax = 127 -> s = 1.0 exactly, so q = rint(x): ties at .5 go to even.
+    row = torch.tensor([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 100.5, -126.5, 0.0, 7.0, 8.5, -8.5, 9.5, 1.0],
+                       dtype=torch.float32)
+    x = row.repeat(4, 1).to(torch.bfloat16)
+    expect = np.array([127, 0, 2, 2, 0, -2, -2, 4, 100, -126, 0, 7, 8, -8, 10, 1], np.int8)
+    xq, s = _hip.act_quant(x.to(_dev()))
+    assert np.all(s.cpu().numpy() == 1.0)
+    np.testing.assert_array_equal(xq.cpu().numpy()[0], expect)
+
+
+# ---------------------------------------------------------------- W8A8
+
+# (M, N, K) covering skinny (M <= 64), tiled, ragged edges and the generic path.
+GEMM_SHAPES = [
+    (1, 4096, 1024), (16, 4096, 1024), (17, 1000, 1024), (48, 6144, 1024), (64, 1024, 3072),
+    (65, 4096, 1024), (256, 4096, 1024), (512, 1024, 3072), (300, 1030, 2048), (129, 136, 80),
+    (7, 33, 40), (3, 5, 1024),
+]
+
+
+def _w8a8_inputs(m, n, k, seed):
+    x = make_activations(m, k, seed=seed)
+    xq, a_s = oracle.c_act_quant(bits16(x))
+    q, w_s = make_weights(n, k, seed=seed + 1)
+    return xq, a_s, q.numpy(), w_s.numpy()
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_w8a8_accumulator_bit_exact(hiplib, shape):
+    from nanovllm.quantization import _hip
+    m, n, k = shape
+    _log_case(test="w8a8_i32", m=m, n=n, k=k, path=_hip.select_path(_hip.OP_W8A8, m, n, k))
+    xq, a_s, q, w_s = _w8a8_inputs(m, n, k, seed=m + n + k)
+    acc = _hip.w8a8_gemm_i32(torch.from_numpy(xq).to(_dev()), torch.from_numpy(q).to(_dev()))
+    np.testing.assert_array_equal(acc.cpu().numpy(), oracle.c_gemm_i32(xq, q))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_w8a8_output(hiplib, shape, out_dtype):
+    from nanovllm.quantization import _hip
+    m, n, k = shape
+    _log_case(test="w8a8_out", m=m, n=n, k=k, dtype=out_dtype)
+    xq, a_s, q, w_s = _w8a8_inputs(m, n, k, seed=3 * m + n + k)
+    d = _dev()
+    y = _hip.w8a8_gemm(torch.from_numpy(xq).to(d), torch.from_numpy(a_s).to(d), torch.from_numpy(q).to(d),
+                       torch.from_numpy(w_s).to(d), None, out_dtype)
+    acc = oracle.c_gemm_i32(xq, q)
+    yb_ref, yf_ref = oracle.c_w8a8_epilogue(acc, a_s, w_s)
+    if out_dtype == torch.bfloat16:
+        np.testing.assert_array_equal(bits16(y), yb_ref)
+    else:
+        np.testing.assert_array_equal(bits16(y), yf_ref.astype(np.float16).view(np.uint16))
+    ref = oracle.w8a8_torch_path(torch.from_numpy(xq), torch.from_numpy(a_s), torch.from_numpy(q),
+                                 torch.from_numpy(w_s), None, out_dtype)
+    assert oracle.rel_l2(f32(y), f32(ref)) <= oracle.REL_L2_TOL
+    assert oracle.max_abs_ratio(f32(y), f32(ref)) <= oracle.MAX_ABS_TOL
+
+
+def test_w8a8_bias(hiplib):
+    from nanovllm.quantization import _hip
+    m, n, k = 80, 264, 1024
+    xq, a_s, q, w_s = _w8a8_inputs(m, n, k, seed=11)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    d = _dev()
+    for mm in (m, 8):  # tiled and skinny
+        y = _hip.w8a8_gemm(torch.from_numpy(xq[:mm]).to(d), torch.from_numpy(a_s[:mm]).to(d),
+                           torch.from_numpy(q).to(d), torch.from_numpy(w_s).to(d), bias.to(d), torch.bfloat16)
+        yb_ref, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq[:mm], q), a_s[:mm], w_s, f32(bias))
+        np.testing.assert_array_equal(bits16(y), yb_ref)
+
+
+def test_w8a8_fused_linear_matches_two_step(hiplib):
+    from nanovllm.quantization import _hip
+    d = _dev()
+    for m in (1, 64, 256, 1000):
+        x = make_activations(m, 1024, seed=m).to(d)
+        q, w_s = make_weights(4096, 1024, seed=9)
+        q, w_s = q.to(d), w_s.to(d)
+        y1 = _hip.w8a8_linear(x, q, w_s)
+        xq, a_s = _hip.act_quant(x)
+        y2 = _hip.w8a8_gemm(xq, a_s, q, w_s, None, torch.bfloat16)
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+# ---------------------------------------------------------------- W8A16
+
+def _w8a16_check(y, x, q, s, bias=None):
+    """Tolerance vs the reference torch path, and a bf16-rounding bound vs fp64."""
+    ref = oracle.w8a16_torch_path(x, q, s, bias)
+    assert oracle.rel_l2(f32(y), f32(ref)) <= oracle.REL_L2_TOL
+    assert oracle.max_abs_ratio(f32(y), f32(ref)) <= oracle.MAX_ABS_TOL
+    y64 = oracle.c_w8a16_f64(bits16(x), q.numpy(), s.numpy(), None if bias is None else f32(bias),
+                             is_bf16=x.dtype == torch.bfloat16)
+    mag = (np.abs(f32(x)).astype(np.float64) @ np.abs(q.numpy()).astype(np.float64).T) * s.numpy()[None, :]
+    k = x.shape[1]
+    half_ulp = 2.0 ** -8 if x.dtype == torch.bfloat16 else 2.0 ** -11
+    bound = np.abs(y64) * half_ulp + mag * (k * 2.0 ** -23) + 1e-30
+    err = np.abs(f32(y).astype(np.float64) - y64)
+    assert np.all(err <= bound), f"max excess {np.max(err - bound)}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_w8a16_output(hiplib, shape, dtype):
+    from nanovllm.quantization import _hip
+    m, n, k = shape
+    _log_case(test="w8a16", m=m, n=n, k=k, dtype=dtype, path=_hip.select_path(_hip.OP_W8A16, m, n, k))
+    x = make_activations(m, k, seed=m * 7 + n + k, dtype=dtype, outlier_frac=0.0)
+    q, s = make_weights(n, k, seed=m + 2 * n + k)
+    d = _dev()
+    y = _hip.w8a16_gemm(x.to(d), q.to(d), s.to(d))
+    _w8a16_check(y, x, q, s)
+
+
+def test_w8a16_bias(hiplib):
+    from nanovllm.quantization import _hip
+    d = _dev()
+    q, s = make_weights(520, 1024, seed=3)
+    bias = torch.randn(520, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    for m in (5, 130):
+        x = make_activations(m, 1024, seed=m, outlier_frac=0.0)
+        y = _hip.w8a16_gemm(x.to(d), q.to(d), s.to(d), bias.to(d))
+        _w8a16_check(y, x, q, s, bias)
+
+
+def test_unaligned_views_take_generic_path(hiplib):
+    """A storage offset that breaks 16-byte alignment must still be correct."""
+    from nanovllm.quantization import _hip
+    d = _dev()
+    m, n, k = 20, 64, 1024
+    xb = make_activations(m * k + 1, 1, seed=1).view(-1)
+    x = xb[1:].view(m, k)  # 2-byte offset
+    q, s = make_weights(n, k, seed=2)
+    y = _hip.w8a16_gemm(xb.to(d)[1:].view(m, k), q.to(d), s.to(d))
+    _w8a16_check(y, x, q, s)
+
+
+# ---------------------------------------------------------------- full-size properties
+
+@pytest.mark.parametrize("mode", ["w8a8", "w8a16"])
+@pytest.mark.parametrize("nk", [(1024, 3072), (1024, 2048), (6144, 1024)])
+def test_prefill_full_size_sampled_rows(hiplib, mode, nk):
+    """M=8192 prefill shapes (config 3): 48 sampled token rows checked exactly /
+    within the bound; the full output checked for finiteness and row-scaling
+    consistency."""
+    from nanovllm.quantization import _hip
+    n, k = nk
+    m = 8192
+    _log_case(test="prefill_full", mode=mode, m=m, n=n, k=k)
+    d = _dev()
+    x = make_activations(m, k, seed=n + k, outlier_frac=0.01 if mode == "w8a8" else 0.0)
+    x[-100:].zero_()  # padded tail rows
+    q, s = make_weights(n, k, seed=k)
+    rows = np.sort(np.random.default_rng(0).choice(m, 48, replace=False))
+    rows[-1] = m - 1
+    if mode == "w8a8":
+        y = _hip.w8a8_linear(x.to(d), q.to(d), s.to(d))
+        xq, a_s = oracle.c_act_quant(bits16(x[torch.from_numpy(rows)]))
+        yb_ref, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq, q.numpy()), a_s, s.numpy())
+        np.testing.assert_array_equal(bits16(y)[rows], yb_ref)
+    else:
+        y = _hip.w8a16_gemm(x.to(d), q.to(d), s.to(d))
+        _w8a16_check(y.cpu()[torch.from_numpy(rows)], x[torch.from_numpy(rows)], q, s)
+    assert torch.isfinite(y.float()).all()
+    assert (y[-100:].float() == 0).all()
+
+
+# ---------------------------------------------------------------- graph capture
+
+def test_hip_graph_capture_replay(hiplib):
+    """The ABI never allocates or syncs, so both GEMMs can be captured and replayed."""
+    from nanovllm.quantization import _hip
+    d = _dev()
+    q, s = make_weights(4096, 1024, seed=1)
+    q, s = q.to(d), s.to(d)
+    x = make_activations(16, 1024, seed=2).to(d)
+    ref16 = _hip.w8a16_gemm(x, q, s)
+    ref8 = _hip.w8a8_linear(x, q, s)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        _hip.w8a16_gemm(x, q, s)  # warm the allocator pools on this stream
+        _hip.w8a8_linear(x, q, s)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y16 = _hip.w8a16_gemm(x, q, s)
+        y8 = _hip.w8a8_linear(x, q, s)
+    for i in range(4):
+        y16.zero_()
+        y8.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y16.view(torch.int16), ref16.view(torch.int16)), f"replay {i}"
+        assert torch.equal(y8.view(torch.int16), ref8.view(torch.int16)), f"replay {i}"

@@ -1,0 +1,313 @@
+"""Pins the oracle (CPU) before it is trusted as the checker.
+
+The reference ships no unit tests, fixtures or golden vectors for this path,
+so each oracle function is pinned by checks a plausible mistake would fail:
+closed-form special cases, brute force on tiny inputs, agreement of the two
+independent restatements (numpy and C), agreement with CPU torch running the
+reference's own expressions, and invariants. Also checks the committed golden
+fixtures (tests/golden/*.npz).
+"""
+from __future__ import annotations
+
+import itertools
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import bits16, f32, make_activations, make_weights
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ------------------------------------------------------------ quantizer
+
+def test_quant_zero_row_gives_eps_scale():
+    q, s = oracle.quantize_rows(np.zeros((2, 16), np.float32))
+    assert s.dtype == np.float32 and np.all(s == np.float32(1e-8))
+    assert np.all(q == 0)
+
+
+def test_quant_single_nonzero_maps_to_127():
+    for v in (3.0, -0.001, 1e20, -7.5):
+        x = np.zeros((1, 9), np.float32)
+        x[0, 4] = v
+        q, s = oracle.quantize_rows(x)
+        assert q[0, 4] == (127 if v > 0 else -127)
+        assert np.count_nonzero(q) == 1
+        assert s[0] == np.float32(abs(np.float32(v)) / np.float32(127.0))
+
+
+def test_quant_amax_element_is_127_for_all_magnitudes():
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        x = rng.standard_normal((1, 64)).astype(np.float32) * np.float32(10.0 ** rng.uniform(-20, 20))
+        q, _ = oracle.quantize_rows(x)
+        i = np.argmax(np.abs(x[0]))
+        assert abs(int(q[0, i])) == 127
+
+
+def test_quant_ties_round_half_to_even():
+    # amax = 127 -> s = 1 exactly, so q = rint(x)
+    x = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 100.5, -126.5, 8.5]], np.float32)
+    q, s = oracle.quantize_rows(x)
+    assert s[0] == 1.0
+    assert q[0].tolist() == [127, 0, 2, 2, 0, -2, -2, 4, 100, -126, 8]
+
+
+def test_quant_power_of_two_scale_ties():
+    # amax = 127 * 2^-3 -> s = 2^-3; x = (k + 0.5) * 2^-3 are exact ties
+    s_exp = 2.0 ** -3
+    ks = np.arange(-20, 20)
+    x = np.concatenate([[127 * s_exp], (ks + 0.5) * s_exp]).astype(np.float32)[None, :]
+    q, s = oracle.quantize_rows(x)
+    assert s[0] == np.float32(s_exp)
+    expect = [int(np.round(k + 0.5)) for k in ks]  # numpy round = half-even
+    assert all(e % 2 == 0 for e in expect)
+    assert q[0, 1:].tolist() == expect
+
+
+def test_quant_never_produces_minus_128_and_clamps():
+    x = np.array([[-1.0, 1.0, -0.999999, 0.3]], np.float32)
+    q, _ = oracle.quantize_rows(x)
+    assert q.min() >= -127
+    x = np.full((3, 5), -2.0, np.float32)
+    q, _ = oracle.quantize_rows(x)
+    assert np.all(q == -127)
+
+
+def test_quant_eps_floor():
+    # amax/127 < eps -> s = eps; values then quantize against eps
+    x = np.array([[1e-10, -5e-10, 0.0]], np.float32)
+    q, s = oracle.quantize_rows(x)
+    assert s[0] == np.float32(1e-8)
+    assert q[0].tolist() == [0, 0, 0]
+    x = np.array([[1e-6 * 127 / 128, 0.5e-8]], np.float32)  # amax/127 just under 1e-8? no: check both sides
+    q, s = oracle.quantize_rows(x)
+    assert s[0] == max(np.float32(x[0, 0]) / np.float32(127.0), np.float32(1e-8))
+
+
+def test_quant_matches_brute_force_python():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((6, 33)) * rng.uniform(0.01, 100, (6, 1))).astype(np.float32)
+    q, s = oracle.quantize_rows(x)
+    for m in range(6):
+        amax = max(abs(float(v)) for v in x[m])
+        sc = np.float32(max(np.float32(amax) / np.float32(127.0), np.float32(1e-8)))
+        assert s[m] == sc
+        for k in range(33):
+            t = float(np.float32(x[m, k]) / sc)  # fp32 divide
+            r = round(t)  # Python round = half-even
+            assert q[m, k] == max(-127, min(127, r))
+
+
+def test_quant_numpy_matches_torch_reference_expression():
+    for seed, (m, k) in enumerate([(64, 1024), (7, 4096), (3, 24)]):
+        x = make_activations(m, k, seed=seed)
+        q_t, s_t = oracle.quantize_rows_torch(x)
+        q_n, s_n = oracle.quantize_rows(f32(x))
+        np.testing.assert_array_equal(q_n, q_t.numpy())
+        np.testing.assert_array_equal(s_n.view(np.uint32), s_t.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quant_c_matches_numpy(dtype):
+    for seed, (m, k) in enumerate([(64, 1024), (9, 3072), (5, 100), (1, 1)]):
+        x = make_activations(m, k, seed=seed, dtype=dtype)
+        if m > 2:
+            x[1].zero_()
+        q_c, s_c = oracle.c_act_quant(bits16(x), is_bf16=dtype == torch.bfloat16)
+        q_n, s_n = oracle.quantize_rows(f32(x))
+        np.testing.assert_array_equal(q_c, q_n)
+        np.testing.assert_array_equal(s_c.view(np.uint32), s_n.view(np.uint32))
+
+
+def test_quant_f32_c_matches_numpy():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((50, 300)) * 0.02).astype(np.float32)
+    q_c, s_c = oracle.c_quant_f32(x)
+    q_n, s_n = oracle.quantize_rows(x)
+    np.testing.assert_array_equal(q_c, q_n)
+    np.testing.assert_array_equal(s_c, s_n)
+
+
+def test_dequant_reconstruction_bound():
+    """|q*s - x| <= s/2 for every element (round-to-nearest invariant)."""
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((20, 512)) * 3).astype(np.float32)
+    q, s = oracle.quantize_rows(x)
+    err = np.abs(q.astype(np.float64) * s[:, None] - x)
+    assert np.all(err <= s[:, None].astype(np.float64) * (0.5 + 1e-6))
+
+
+def test_f16_decoder_matches_numpy():
+    bits = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    fin = np.isfinite(bits.view(np.float16))
+    x = bits.reshape(256, 256)
+    q_c, s_c = oracle.c_act_quant(np.where(fin, bits, 0).astype(np.uint16).reshape(256, 256), is_bf16=False)
+    q_n, s_n = oracle.quantize_rows(oracle.f16_bits_to_f32(np.where(fin, bits, 0).reshape(256, 256)))
+    np.testing.assert_array_equal(q_c, q_n)
+    np.testing.assert_array_equal(s_c, s_n)
+    del x
+
+
+# ------------------------------------------------------------ bf16 rounding
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(5)
+    v = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 1e3,
+                        np.array([0.0, -0.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 3.0e38, -1e-40], np.float32)])
+    ref = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(oracle.f32_to_bf16_bits(v), ref)
+    np.testing.assert_array_equal(oracle.c_f32_to_bf16(v), ref)
+
+
+# ------------------------------------------------------------ int32 accumulator
+
+def test_gemm_i32_brute_force_tiny():
+    rng = np.random.default_rng(6)
+    for m, n, k in [(1, 1, 1), (2, 3, 5), (4, 7, 16), (3, 2, 33)]:
+        a = rng.integers(-127, 128, (m, k)).astype(np.int8)
+        b = rng.integers(-127, 128, (n, k)).astype(np.int8)
+        expect = [[sum(int(a[i, t]) * int(b[j, t]) for t in range(k)) for j in range(n)] for i in range(m)]
+        np.testing.assert_array_equal(oracle.gemm_i32(a, b), np.array(expect, np.int32))
+        np.testing.assert_array_equal(oracle.c_gemm_i32(a, b), np.array(expect, np.int32))
+
+
+def test_gemm_i32_extremes_and_identity():
+    k = 12288  # largest K in the configs: |acc| <= 127^2 * K < 2^31
+    a = np.full((2, k), 127, np.int8)
+    a[1] = -127
+    b = np.full((3, k), -127, np.int8)
+    acc = oracle.c_gemm_i32(a, b)
+    assert acc[0, 0] == -127 * 127 * k and acc[1, 0] == 127 * 127 * k
+    eye = np.eye(16, dtype=np.int8)
+    x = np.random.default_rng(7).integers(-127, 128, (5, 16)).astype(np.int8)
+    np.testing.assert_array_equal(oracle.c_gemm_i32(x, eye), x.astype(np.int32))
+
+
+def test_gemm_i32_c_matches_numpy_and_linearity():
+    rng = np.random.default_rng(8)
+    a = rng.integers(-60, 61, (37, 200)).astype(np.int8)
+    a2 = rng.integers(-60, 61, (37, 200)).astype(np.int8)
+    b = rng.integers(-127, 128, (29, 200)).astype(np.int8)
+    c1 = oracle.c_gemm_i32(a, b)
+    np.testing.assert_array_equal(c1, oracle.gemm_i32(a, b))
+    c12 = oracle.c_gemm_i32((a.astype(np.int16) + a2).astype(np.int8), b)
+    np.testing.assert_array_equal(c12, c1 + oracle.c_gemm_i32(a2, b))
+    # transpose symmetry: (A B^T)^T = B A^T
+    np.testing.assert_array_equal(oracle.c_gemm_i32(b, a), c1.T)
+
+
+# ------------------------------------------------------------ W8A8 epilogue
+
+def test_w8a8_epilogue_c_matches_numpy_and_fp64():
+    rng = np.random.default_rng(9)
+    acc = rng.integers(-(2 ** 28), 2 ** 28, (40, 50)).astype(np.int32)
+    a_s = (rng.uniform(0.001, 1.0, 40)).astype(np.float32)
+    w_s = (rng.uniform(1e-5, 1e-3, 50)).astype(np.float32)
+    yb, yf = oracle.c_w8a8_epilogue(acc, a_s, w_s)
+    np.testing.assert_array_equal(yf, oracle.w8a8_epilogue_f32(acc, a_s, w_s))
+    np.testing.assert_array_equal(yb, oracle.w8a8_epilogue_bf16(acc, a_s, w_s))
+    exact = acc.astype(np.float64) * a_s[:, None] * w_s[None, :]
+    assert np.all(np.abs(yf - exact) <= np.abs(exact) * 2.0 ** -22)
+    got = oracle.bf16_bits_to_f32(yb).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= np.abs(exact) * (2.0 ** -8 + 2.0 ** -21))
+
+
+def test_w8a8_epilogue_zero_sign_and_order():
+    acc = np.array([[0, -1, 1, 3]], np.int32)
+    a_s = np.array([0.5], np.float32)
+    w_s = np.array([2.0, -0.0, 4.0, 1.0 / 3.0], np.float32)
+    yb, yf = oracle.c_w8a8_epilogue(acc, a_s, w_s)
+    # (0*0.5)*2 + 0 = +0; (-1*0.5)*-0 = +0 then + 0 -> +0 bits
+    assert yb[0, 0] == 0 and yb[0, 1] == 0
+    assert yf[0, 2] == 2.0
+    # order: (3*0.5)*(1/3) rounded per step in fp32
+    assert yf[0, 3] == np.float32(np.float32(1.5) * np.float32(1.0 / 3.0))
+
+
+def test_w8a8_epilogue_bias_is_fused_fma():
+    acc = np.array([[1 << 24 | 1]], np.int32)
+    a_s = np.array([1.0], np.float32)
+    w_s = np.array([1.0 + 2.0 ** -23], np.float32)
+    bias = np.array([-float(np.float32((1 << 24 | 1)))], np.float32)
+    _, yf = oracle.c_w8a8_epilogue(acc, a_s, w_s, bias)
+    p = np.float64(np.float32(1 << 24 | 1))  # float(acc) rounds to 16777216
+    assert yf[0, 0] == np.float32(p * (1.0 + 2.0 ** -23) + float(bias[0]))  # exact fma result
+
+
+# ------------------------------------------------------------ torch paths
+
+def test_w8a16_torch_path_close_to_exact():
+    x = make_activations(32, 1024, seed=10, outlier_frac=0.0)
+    q, s = make_weights(256, 1024, seed=11)
+    y = oracle.w8a16_torch_path(x, q, s)
+    y64 = oracle.w8a16_f64(f32(x), q.numpy(), s.numpy())
+    assert oracle.rel_l2(f32(y), y64) < 5e-3
+    y64c = oracle.c_w8a16_f64(bits16(x), q.numpy(), s.numpy())
+    np.testing.assert_allclose(y64c, y64, rtol=1e-12, atol=1e-12)
+
+
+def test_w8a16_f64_brute_force():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((3, 5)).astype(np.float32)
+    xb = oracle.f32_to_bf16_bits(x)
+    xr = oracle.bf16_bits_to_f32(xb)
+    q = rng.integers(-127, 128, (4, 5)).astype(np.int8)
+    s = rng.uniform(0.01, 0.1, 4).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    y = oracle.c_w8a16_f64(xb, q, s, b)
+    for i, j in itertools.product(range(3), range(4)):
+        e = sum(float(xr[i, t]) * int(q[j, t]) for t in range(5)) * float(s[j]) + float(b[j])
+        assert abs(y[i, j] - e) <= 1e-12 * max(1.0, abs(e))
+
+
+def test_w8a8_torch_path_close_to_exact():
+    x = make_activations(64, 1024, seed=13)
+    xq, a_s = oracle.quantize_rows(f32(x))
+    q, w_s = make_weights(128, 1024, seed=14)
+    y = oracle.w8a8_torch_path(torch.from_numpy(xq), torch.from_numpy(a_s), q, w_s, None, torch.bfloat16)
+    y64 = oracle.w8a8_f64(xq, a_s, q.numpy(), w_s.numpy())
+    assert oracle.rel_l2(f32(y), y64) < 1e-2
+    # and the bit-exact kernel epilogue is closer to exact than the torch path
+    yb, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq, q.numpy()), a_s, w_s.numpy())
+    assert oracle.rel_l2(oracle.bf16_bits_to_f32(yb), y64) <= oracle.rel_l2(f32(y), y64)
+
+
+# ------------------------------------------------------------ golden fixtures
+
+def _golden_files():
+    return sorted(GOLDEN.glob("*.npz"))
+
+
+def test_golden_fixtures_present():
+    assert _golden_files(), "tests/golden/*.npz missing; run tests/golden/make_golden.py"
+
+
+@pytest.mark.parametrize("path", _golden_files(), ids=lambda p: p.stem)
+def test_golden_fixture(path):
+    d = np.load(path, allow_pickle=False)
+    kind = str(d["kind"])
+    if kind == "act_quant":
+        q, s = oracle.c_act_quant(d["x_bits"], is_bf16=bool(d["is_bf16"]))
+        np.testing.assert_array_equal(q, d["xq"])
+        np.testing.assert_array_equal(s.view(np.uint32), d["a_scales"].view(np.uint32))
+        q2, s2 = oracle.quantize_rows(oracle.to_f32(d["x_bits"], bool(d["is_bf16"])))
+        np.testing.assert_array_equal(q2, d["xq"])
+    elif kind == "w8a8":
+        acc = oracle.c_gemm_i32(d["xq"], d["qweight"])
+        np.testing.assert_array_equal(acc, d["acc"])
+        yb, _ = oracle.c_w8a8_epilogue(acc, d["a_scales"], d["w_scales"])
+        np.testing.assert_array_equal(yb, d["y_bits"])
+    elif kind == "w8a16":
+        y = oracle.c_w8a16_f64(d["x_bits"], d["qweight"], d["scales"])
+        np.testing.assert_allclose(y, d["y_f64"], rtol=1e-12, atol=1e-12)
+    elif kind == "kat":
+        q, s = oracle.quantize_rows(d["x"])
+        np.testing.assert_array_equal(q, d["q"])
+        np.testing.assert_array_equal(s, d["s"])
+    else:
+        pytest.fail(f"unknown fixture kind {kind}")

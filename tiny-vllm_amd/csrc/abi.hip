@@ -1,0 +1,160 @@
+// C ABI of libtinyvllm_quant.so: argument validation, the M-bucketed path
+// selection and the launches. Declared in include/tvq.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/tvq.h"
+#include "tvq_internal.h"
+
+namespace tvq {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return TVQ_OK;
+}
+
+constexpr int64_t kMaxDim = 0x7fffffff;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_dims(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(TVQ_E_INVALID, "invalid shape M=%lld N=%lld K=%lld", (long long)M,
+                                             (long long)N, (long long)K);
+  if (M > kMaxDim || N > kMaxDim || K > kMaxDim)
+    return fail(TVQ_E_UNSUPPORTED, "dimension exceeds 2^31-1: M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                (long long)K);
+  return TVQ_OK;
+}
+
+int check_dtype(int dtype) {
+  if (dtype != TVQ_DTYPE_F16 && dtype != TVQ_DTYPE_BF16)
+    return fail(TVQ_E_INVALID, "dtype must be TVQ_DTYPE_F16 (0) or TVQ_DTYPE_BF16 (1), got %d", dtype);
+  return TVQ_OK;
+}
+
+bool shape_vec_ok(int64_t K) { return K % 16 == 0; }
+
+int run_gemm(const GemmArgs& a, void* stream) {
+  if (a.M == 0) return ok();
+  hipError_t e;
+  switch (select_gemm_path(a)) {
+    case Path::kSkinny: e = launch_skinny(a, (hipStream_t)stream); break;
+    case Path::kTiled: e = launch_tiled(a, (hipStream_t)stream); break;
+    default: e = launch_generic(a, (hipStream_t)stream); break;
+  }
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+Path select_gemm_path(const GemmArgs& a) {
+  const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
+  if (!aligned) return Path::kGeneric;
+  return a.M <= kSkinnyMaxM ? Path::kSkinny : Path::kTiled;
+}
+
+const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
+  (void)N;
+  if (!aligned || !shape_vec_ok(K)) return "generic_simt";
+  if (M <= kSkinnyMaxM) {
+    static const char* names8[4] = {"skinny_mfma_i8_m16", "skinny_mfma_i8_m32", "skinny_mfma_i8_m48",
+                                    "skinny_mfma_i8_m64"};
+    static const char* names16[4] = {"skinny_mfma_f16x_m16", "skinny_mfma_f16x_m32", "skinny_mfma_f16x_m48",
+                                     "skinny_mfma_f16x_m64"};
+    const int mg = M <= 0 ? 0 : (int)((M + 15) / 16) - 1;
+    return w8a8 ? names8[mg] : names16[mg];
+  }
+  return w8a8 ? "tiled_mfma_i8_128x128x128" : "tiled_mfma_f16x_128x128x64";
+}
+
+}  // namespace tvq
+
+using namespace tvq;
+
+extern "C" {
+
+int tvq_abi_version(void) { return TVQ_ABI_VERSION; }
+
+const char* tvq_last_error(void) { return g_last_error.c_str(); }
+
+const char* tvq_select_path(int op, int64_t M, int64_t N, int64_t K, int dtype) {
+  (void)dtype;
+  switch (op) {
+    case TVQ_OP_ACT_QUANT: return (K % 8 == 0) ? "act_quant_vec" : "act_quant_scalar";
+    case TVQ_OP_W8A16: return gemm_path_name(false, M, N, K, true);
+    case TVQ_OP_W8A8: return gemm_path_name(true, M, N, K, true);
+    default: return nullptr;
+  }
+}
+
+int tvq_act_quant(const void* x, int dtype, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
+                  void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dims(M, 1, K)) return rc;
+  if (M == 0) return ok();
+  if (!x || !xq || !a_scales) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (!(eps >= 0.0f)) return fail(TVQ_E_INVALID, "eps must be >= 0");
+  hipError_t e = launch_act_quant(x, dtype == TVQ_DTYPE_BF16, M, K, eps, xq, a_scales, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "act_quant launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight, const float* scales, const void* bias, void* y,
+                   int64_t M, int64_t N, int64_t K, void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dims(M, N, K)) return rc;
+  if (M == 0) return ok();
+  if (!x || !qweight || !scales || !y) return fail(TVQ_E_INVALID, "null pointer argument");
+  GemmArgs a{x, nullptr, qweight, scales, bias, y, M, N, K, false, dtype == TVQ_DTYPE_BF16, false};
+  return run_gemm(a, stream);
+}
+
+int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales, const int8_t* qweight, const float* w_scales,
+                  const void* bias, void* y, int out_dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (int rc = check_dtype(out_dtype)) return rc;
+  if (int rc = check_dims(M, N, K)) return rc;
+  if (M == 0) return ok();
+  if (!xq || !a_scales || !qweight || !w_scales || !y) return fail(TVQ_E_INVALID, "null pointer argument");
+  GemmArgs a{xq, a_scales, qweight, w_scales, bias, y, M, N, K, true, out_dtype == TVQ_DTYPE_BF16, false};
+  return run_gemm(a, stream);
+}
+
+int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32, int64_t M, int64_t N, int64_t K,
+                      void* stream) {
+  if (int rc = check_dims(M, N, K)) return rc;
+  if (M == 0) return ok();
+  if (!xq || !qweight || !y_i32) return fail(TVQ_E_INVALID, "null pointer argument");
+  GemmArgs a{xq, nullptr, qweight, nullptr, nullptr, y_i32, M, N, K, true, true, true};
+  return run_gemm(a, stream);
+}
+
+int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight, const float* w_scales, const void* bias,
+                    void* y, int64_t M, int64_t N, int64_t K, int8_t* xq_buf, float* a_scales_buf, void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dims(M, N, K)) return rc;
+  if (M == 0) return ok();
+  if (!x || !qweight || !w_scales || !y || !xq_buf || !a_scales_buf)
+    return fail(TVQ_E_INVALID, "null pointer argument");
+  if (int rc = tvq_act_quant(x, dtype, M, K, 1e-8f, xq_buf, a_scales_buf, stream)) return rc;
+  return tvq_w8a8_gemm(xq_buf, a_scales_buf, qweight, w_scales, bias, y, dtype, M, N, K, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,215 @@
+// Skinny (decode-size M <= 64) W8A16 / W8A8 GEMM for gfx950.
+//
+// Decode is weight-bandwidth bound: every int8 weight byte is read exactly
+// once and the activations are tiny and L2-resident. The kernel therefore
+// streams qweight [N,K] with 128-bit non-temporal loads and puts the weight
+// rows on the MFMA "A" side (16 output channels per MFMA block) and the
+// activation rows on the "B" side (16 tokens per block):
+//
+//   lane l = 16*g + r reads 16 consecutive int8 of weight row n0+r at
+//   k = kc + 16*g, and the same k range of token row r of x.
+//
+// W8A8  : one v_mfma_i32_16x16x64_i8 consumes the 16 bytes directly (exact
+//         int32 accumulation).
+// W8A16 : the 16 bytes are converted in registers to two 8-element bf16/fp16
+//         fragments (int8 is exact in both) and feed two
+//         v_mfma_f32_16x16x32_{bf16,f16}. The fp32 per-channel scale is
+//         applied once per output in the epilogue instead of per weight.
+//
+// Any consistent assignment of k to (lane group, register slot) yields the
+// same dot products, so A and B only have to agree with each other.
+//
+// A 256-thread workgroup owns 16*RG output channels; its 4 waves split K in
+// interleaved runs of U 64-wide chunks and are reduced through LDS at the
+// end, so the whole reduction order is fixed (deterministic output).
+#include "tvq_common.h"
+#include "tvq_internal.h"
+
+namespace tvq {
+namespace {
+
+constexpr int kWaves = 4;
+
+template <int MG, int RG>
+struct SkinnyCfg {
+  // Chunks in flight per wave: bounded so weight + activation registers stay
+  // around 64 VGPRs.
+  static constexpr int U = (8 / (RG * MG)) > 0 ? (8 / (RG * MG)) : 1;
+};
+
+template <typename T, bool kW8A8, bool kRaw, int MG, int RG>
+__global__ __launch_bounds__(256) void skinny_kernel(const void* __restrict__ xv, const float* __restrict__ a_scales,
+                                                     const int8_t* __restrict__ qw, const float* __restrict__ ws,
+                                                     const uint16_t* __restrict__ bias, void* __restrict__ yv,
+                                                     int M, int N, int K) {
+  constexpr int U = SkinnyCfg<MG, RG>::U;
+  using Acc = typename std::conditional<kW8A8, i32x4, f32x4>::type;
+  constexpr int kXRegs = kW8A8 ? 1 : 2;  // 16-byte x vectors per (chunk, m-group)
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int n0 = blockIdx.x * (16 * RG);
+
+  Acc acc[RG][MG];
+#pragma unroll
+  for (int i = 0; i < RG; ++i)
+#pragma unroll
+    for (int j = 0; j < MG; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+
+  // Per-lane row pointers (clamped rows are never dereferenced).
+  const int8_t* wrow[RG];
+  bool wok[RG];
+#pragma unroll
+  for (int i = 0; i < RG; ++i) {
+    const int n = n0 + 16 * i + r;
+    wok[i] = n < N;
+    wrow[i] = qw + (int64_t)(wok[i] ? n : 0) * K + 16 * g;
+  }
+  const char* xrow[MG];
+  bool xok[MG];
+#pragma unroll
+  for (int j = 0; j < MG; ++j) {
+    const int m = 16 * j + r;
+    xok[j] = m < M;
+    xrow[j] = static_cast<const char*>(xv) + (int64_t)(xok[j] ? m : 0) * K * (kW8A8 ? 1 : 2) + 16 * g * (kW8A8 ? 1 : 2);
+  }
+
+  const int nchunks = (K + 63) >> 6;
+  for (int c0 = wave * U; c0 < nchunks; c0 += kWaves * U) {
+    u32x4 wv[U][RG];
+    u32x4 xvv[U][MG][kXRegs];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kb = (c0 + u) * 64 + 16 * g;  // first k of this lane's 16-k slice
+      const bool kok = kb < K;
+#pragma unroll
+      for (int i = 0; i < RG; ++i)
+        wv[u][i] = (kok && wok[i]) ? ldg128_stream(wrow[i] + (int64_t)(c0 + u) * 64) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < MG; ++j) {
+#pragma unroll
+        for (int h = 0; h < kXRegs; ++h) {
+          const int64_t off = (int64_t)(c0 + u) * 64 * (kW8A8 ? 1 : 2) + 16 * h;
+          xvv[u][j][h] = (kok && xok[j]) ? ldg128(xrow[j] + off) : u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int i = 0; i < RG; ++i) {
+        if constexpr (kW8A8) {
+#pragma unroll
+          for (int j = 0; j < MG; ++j) acc[i][j] = mfma16x16x64_i8(wv[u][i], xvv[u][j][0], acc[i][j]);
+        } else {
+          const u32x2 a0 = i8x4_to_16x4<T>(wv[u][i][0]);
+          const u32x2 a1 = i8x4_to_16x4<T>(wv[u][i][1]);
+          const u32x2 a2 = i8x4_to_16x4<T>(wv[u][i][2]);
+          const u32x2 a3 = i8x4_to_16x4<T>(wv[u][i][3]);
+          const u32x4 alo = {a0.x, a0.y, a1.x, a1.y};
+          const u32x4 ahi = {a2.x, a2.y, a3.x, a3.y};
+#pragma unroll
+          for (int j = 0; j < MG; ++j) {
+            acc[i][j] = mfma16x16x32<T>(alo, xvv[u][j][0], acc[i][j]);
+            acc[i][j] = mfma16x16x32<T>(ahi, xvv[u][j][1], acc[i][j]);
+          }
+        }
+      }
+    }
+  }
+
+  // Cross-wave reduction in a fixed order (wave 0 + 1 + 2 + 3).
+  __shared__ Acc red[kWaves][RG * MG][64];
+#pragma unroll
+  for (int i = 0; i < RG; ++i)
+#pragma unroll
+    for (int j = 0; j < MG; ++j) red[wave][i * MG + j][lane] = acc[i][j];
+  __syncthreads();
+
+  constexpr int kItems = RG * MG * 64;
+  for (int it = tid; it < kItems; it += 256) {
+    const int ij = it >> 6;
+    const int ln = it & 63;
+    const int i = ij / MG;
+    const int j = ij % MG;
+    Acc v = red[0][ij][ln];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += red[w][ij][ln];
+    const int m = 16 * j + (ln & 15);
+    const int nb = n0 + 16 * i + 4 * (ln >> 4);
+    if (m >= M) continue;
+    if constexpr (kRaw) {
+      int32_t* y = static_cast<int32_t*>(yv) + (int64_t)m * N;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (nb + t < N) y[nb + t] = v[t];
+    } else {
+      uint16_t* y = static_cast<uint16_t*>(yv) + (int64_t)m * N;
+      float o[4];
+      float as = 0.0f;
+      if constexpr (kW8A8) as = a_scales[m];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int n = nb + t < N ? nb + t : N - 1;
+        const float b = bias ? to_float<T>(bias[n]) : 0.0f;
+        if constexpr (kW8A8)
+          o[t] = epi_w8a8(v[t], as, ws[n], b);
+        else
+          o[t] = epi_w8a16(v[t], ws[n], b);
+      }
+      if (nb + 3 < N && (N & 3) == 0) {
+        u32x2 pk;
+        pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
+        pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
+        *reinterpret_cast<u32x2*>(y + nb) = pk;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (nb + t < N) y[nb + t] = from_float<T>(o[t]);
+      }
+    }
+  }
+}
+
+template <typename T, bool kW8A8, bool kRaw, int MG>
+hipError_t launch_mg(const GemmArgs& a, hipStream_t stream) {
+  // Two row groups per wave only when that still leaves >= 4 workgroups per CU.
+  const bool rg2 = a.N >= 16 * 2 * 1024;
+  const int rows = rg2 ? 32 : 16;
+  const dim3 grid((unsigned)((a.N + rows - 1) / rows));
+  const dim3 block(256);
+  const uint16_t* bias = static_cast<const uint16_t*>(a.bias);
+  if (rg2)
+    skinny_kernel<T, kW8A8, kRaw, MG, 2><<<grid, block, 0, stream>>>(a.x, a.a_scales, a.qweight, a.scales, bias, a.y,
+                                                                       (int)a.M, (int)a.N, (int)a.K);
+  else
+    skinny_kernel<T, kW8A8, kRaw, MG, 1><<<grid, block, 0, stream>>>(a.x, a.a_scales, a.qweight, a.scales, bias, a.y,
+                                                                       (int)a.M, (int)a.N, (int)a.K);
+  return hipGetLastError();
+}
+
+template <typename T, bool kW8A8, bool kRaw>
+hipError_t launch_t(const GemmArgs& a, hipStream_t stream) {
+  const int mg = (int)((a.M + 15) / 16);
+  switch (mg) {
+    case 1: return launch_mg<T, kW8A8, kRaw, 1>(a, stream);
+    case 2: return launch_mg<T, kW8A8, kRaw, 2>(a, stream);
+    case 3: return launch_mg<T, kW8A8, kRaw, 3>(a, stream);
+    default: return launch_mg<T, kW8A8, kRaw, 4>(a, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_skinny(const GemmArgs& a, hipStream_t stream) {
+  if (a.w8a8) {
+    if (a.raw_i32) return launch_t<BF16, true, true>(a, stream);
+    return a.bf16 ? launch_t<BF16, true, false>(a, stream) : launch_t<F16, true, false>(a, stream);
+  }
+  return a.bf16 ? launch_t<BF16, false, false>(a, stream) : launch_t<F16, false, false>(a, stream);
+}
+
+}  // namespace tvq

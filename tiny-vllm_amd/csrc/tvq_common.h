@@ -1,0 +1,117 @@
+// Shared device helpers for the gfx950 quantized-linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tvq {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+// Element-type tags. Activations / outputs are stored as raw 16-bit words.
+struct BF16 {
+  static constexpr bool kIsBF16 = true;
+};
+struct F16 {
+  static constexpr bool kIsBF16 = false;
+};
+
+template <typename T>
+__device__ __forceinline__ float to_float(uint16_t h);
+template <>
+__device__ __forceinline__ float to_float<BF16>(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+template <>
+__device__ __forceinline__ float to_float<F16>(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Round-to-nearest-even float -> 16-bit (matches c10::BFloat16 / c10::Half).
+template <typename T>
+__device__ __forceinline__ uint16_t from_float(float f);
+template <>
+__device__ __forceinline__ uint16_t from_float<BF16>(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+template <>
+__device__ __forceinline__ uint16_t from_float<F16>(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Four signed int8 packed in a dword -> four 16-bit floats (bf16 or fp16),
+// packed two per dword. |q| <= 128 is exact in both formats. For bf16 the
+// fp32 value has a zero low half, so taking the high half is exact; the
+// int->float conversion compiles to one SDWA v_cvt_f32_i32 per byte.
+template <typename T>
+__device__ __forceinline__ u32x2 i8x4_to_16x4(uint32_t w);
+template <>
+__device__ __forceinline__ u32x2 i8x4_to_16x4<BF16>(uint32_t w) {
+  const float f0 = (float)(int8_t)(w);
+  const float f1 = (float)(int8_t)(w >> 8);
+  const float f2 = (float)(int8_t)(w >> 16);
+  const float f3 = (float)((int32_t)w >> 24);
+  u32x2 r;
+  // byte selector 0x07060302: high half of src0 (bytes 6,7) over high half of
+  // src1 (bytes 2,3) -> {lo = bf16(f0), hi = bf16(f1)}.
+  r.x = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
+  r.y = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f3), __builtin_bit_cast(uint32_t, f2), 0x07060302u);
+  return r;
+}
+template <>
+__device__ __forceinline__ u32x2 i8x4_to_16x4<F16>(uint32_t w) {
+  const _Float16 h0 = (_Float16)(int8_t)(w);
+  const _Float16 h1 = (_Float16)(int8_t)(w >> 8);
+  const _Float16 h2 = (_Float16)(int8_t)(w >> 16);
+  const _Float16 h3 = (_Float16)((int32_t)w >> 24);
+  u32x2 r;
+  r.x = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+  r.y = (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
+  return r;
+}
+
+// One 16x16x32 MFMA on 16-bit operands held as four dwords (eight elements).
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// One 16x16x64 int8 MFMA with exact int32 accumulation.
+__device__ __forceinline__ i32x4 mfma16x16x64_i8(u32x4 a, u32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 ldg128(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Streaming (read-once) 128-bit load: non-temporal so weights that are read
+// exactly once do not evict the activations other workgroups re-read.
+__device__ __forceinline__ u32x4 ldg128_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// Kernel epilogues. Both apply the per-output-channel fp32 scale once per
+// output element, after the dot product.
+//   W8A16: y = acc * s[n] + bias[n]
+//   W8A8 : y = (float(acc) * a_s[m]) * w_s[n] + bias[n]   (w8a8_gemm.cu:387-390
+//          order; the bias add is fused as one fma, as nvcc contracts it)
+__device__ __forceinline__ float epi_w8a16(float acc, float s, float b) { return __builtin_fmaf(acc, s, b); }
+__device__ __forceinline__ float epi_w8a8(int32_t acc, float as, float ws, float b) {
+  return __builtin_fmaf((float)acc * as, ws, b);
+}
+
+}  // namespace tvq

@@ -1,0 +1,44 @@
+// Host-side launch helpers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tvq {
+
+// Kernel families chosen by the M-bucketed dispatcher.
+enum class Path : int {
+  kGeneric = 0,  // scalar reference-order kernel: any K, any alignment
+  kSkinny = 1,   // M <= 64: weight-streaming MFMA GEMV / skinny GEMM
+  kTiled = 2,    // M > 64: LDS double-buffered MFMA tiles
+};
+
+struct GemmArgs {
+  const void* x;         // W8A16: [M,K] 16-bit; W8A8: [M,K] int8
+  const float* a_scales; // W8A8 only
+  const int8_t* qweight; // [N,K]
+  const float* scales;   // [N]
+  const void* bias;      // [N] 16-bit or nullptr
+  void* y;               // [M,N] 16-bit, or int32 when raw_i32
+  int64_t M, N, K;
+  bool w8a8;
+  bool bf16;     // activation (W8A16) / output (W8A8) element type
+  bool raw_i32;  // W8A8 only: write the int32 accumulator instead of y
+};
+
+bool act_quant_vec_ok(const void* x, const void* xq, int64_t K);
+hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
+                            hipStream_t stream);
+
+// Path selection (pure function of shape and pointer alignment).
+Path select_gemm_path(const GemmArgs& a);
+const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned);
+
+hipError_t launch_skinny(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_tiled(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_generic(const GemmArgs& a, hipStream_t stream);
+
+// Largest M served by the skinny family.
+constexpr int64_t kSkinnyMaxM = 64;
+
+}  // namespace tvq

@@ -1,0 +1,243 @@
+"""ctypes binding of libtinyvllm_quant.so (include/tvq.h) plus thin torch-facing
+wrappers that validate tensors, allocate outputs with torch's caching allocator
+and launch on the current HIP stream.
+
+This module replaces the reference's JIT-built pybind11 extensions
+(nanovllm/quantization/cuda.py:146-222 loaders; csrc/*.cpp `forward` /
+`select_path`). Nothing here computes on the CPU: if the library is missing or
+a call fails, a RuntimeError is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_NAME = "libtinyvllm_quant.so"
+ABI_VERSION = 1
+
+OP_ACT_QUANT = 0
+OP_W8A16 = 1
+OP_W8A8 = 2
+
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+
+_TORCH_TO_TVQ = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+# (name, restype, argtypes) for every symbol include/tvq.h declares.
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+SYMBOLS = (
+    ("tvq_abi_version", _INT, ()),
+    ("tvq_last_error", ctypes.c_char_p, ()),
+    ("tvq_select_path", ctypes.c_char_p, (_INT, _I64, _I64, _I64, _INT)),
+    ("tvq_act_quant", _INT, (_VP, _INT, _I64, _I64, ctypes.c_float, _VP, _VP, _VP)),
+    ("tvq_w8a16_gemm", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP)),
+    ("tvq_w8a8_gemm", _INT, (_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP)),
+    ("tvq_w8a8_gemm_i32", _INT, (_VP, _VP, _VP, _I64, _I64, _I64, _VP)),
+    ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP)),
+)
+
+
+def library_path() -> Path:
+    """Location of the built library: $TVQ_LIBRARY, else tiny-vllm_amd/lib/."""
+    env = os.environ.get("TVQ_LIBRARY")
+    if env:
+        return Path(env)
+    return Path(__file__).resolve().parents[2] / "lib" / LIB_NAME
+
+
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load (once) and type the C ABI. Raises RuntimeError if it is missing."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = library_path()
+        if not path.is_file():
+            raise RuntimeError(
+                f"{LIB_NAME} not found at {path}; build it with `python tiny-vllm_amd/build.py` "
+                "(or __graft_entry__.build())"
+            )
+        try:
+            lib = ctypes.CDLL(str(path))
+        except OSError as exc:
+            raise RuntimeError(f"failed to load {path}: {exc}") from exc
+        for name, restype, argtypes in SYMBOLS:
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = list(argtypes)
+        version = lib.tvq_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+        _LIB = lib
+        return lib
+
+
+def is_available() -> bool:
+    try:
+        load_library()
+    except RuntimeError:
+        return False
+    return True
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().tvq_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        _require(t.is_cuda, "all tensors must be on a ROCm (cuda) device")
+        _require(t.is_contiguous(), "all tensors must be contiguous")
+        if dev is None:
+            dev = t.device
+        _require(t.device == dev, "all tensors must be on the same device")
+    return dev
+
+
+def select_path(op: int, m: int, n: int, k: int, dtype: torch.dtype = torch.bfloat16) -> str:
+    """Kernel path name for an op and shape (M-bucketed dispatch)."""
+    res = load_library().tvq_select_path(op, m, n, k, _TORCH_TO_TVQ.get(dtype, DTYPE_BF16))
+    _require(res is not None, f"invalid op {op}")
+    return res.decode()
+
+
+def act_quant(x: torch.Tensor, eps: float = 1e-8) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row dynamic int8 quantization of a 2-D bf16/fp16 tensor on the GPU."""
+    lib = load_library()
+    dev = _require_gpu(x)
+    _require(x.dim() == 2, "x must be 2-D")
+    _require(x.dtype in _TORCH_TO_TVQ, "x must be float16 or bfloat16")
+    m, k = x.shape
+    xq = torch.empty((m, k), dtype=torch.int8, device=dev)
+    scales = torch.empty((m,), dtype=torch.float32, device=dev)
+    if m == 0:
+        return xq, scales
+    _require(k > 0, "x must have K > 0")
+    with torch.cuda.device(dev):
+        rc = lib.tvq_act_quant(x.data_ptr(), _TORCH_TO_TVQ[x.dtype], m, k, eps, xq.data_ptr(), scales.data_ptr(),
+                               _stream(dev))
+    _check(rc, "tvq_act_quant")
+    return xq, scales
+
+
+def _check_weight(qweight: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None, k: int,
+                  out_dtype: torch.dtype) -> int:
+    _require(qweight.dim() == 2 and qweight.dtype == torch.int8, "qweight must be a 2-D int8 tensor")
+    _require(qweight.shape[1] == k, f"Incompatible shapes: x[-1]={k} vs qweight[-1]={qweight.shape[1]}")
+    n = qweight.shape[0]
+    _require(scales.dim() == 1 and scales.dtype == torch.float32 and scales.numel() == n,
+             "scales must be 1D float32 with one value per output channel")
+    if bias is not None:
+        _require(bias.dim() == 1 and bias.numel() == n, "bias must be 1D with one value per output channel")
+        _require(bias.dtype == out_dtype, "bias dtype must match the output dtype")
+    return n
+
+
+def w8a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+               bias: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M,N] = x[M,K] @ (qweight * scales[:,None])^T + bias, on the GPU."""
+    lib = load_library()
+    dev = _require_gpu(x, qweight, scales, bias)
+    _require(x.dim() == 2, "x must be 2-D")
+    _require(x.dtype in _TORCH_TO_TVQ, "x must be float16 or bfloat16")
+    m, k = x.shape
+    n = _check_weight(qweight, scales, bias, k, x.dtype)
+    y = torch.empty((m, n), dtype=x.dtype, device=dev)
+    if m == 0:
+        return y
+    with torch.cuda.device(dev):
+        rc = lib.tvq_w8a16_gemm(x.data_ptr(), _TORCH_TO_TVQ[x.dtype], qweight.data_ptr(), scales.data_ptr(),
+                                _ptr(bias), y.data_ptr(), m, n, k, _stream(dev))
+    _check(rc, "tvq_w8a16_gemm")
+    return y
+
+
+def w8a8_gemm(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
+              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """y = ((x_q @ qweight^T) * a_scales[:,None]) * w_scales[None,:] + bias, int32 accumulation."""
+    lib = load_library()
+    dev = _require_gpu(x_q, a_scales, qweight, w_scales, bias)
+    _require(out_dtype in _TORCH_TO_TVQ, "out_dtype must be float16 or bfloat16")
+    _require(x_q.dim() == 2 and x_q.dtype == torch.int8, "x_q must be a 2-D int8 tensor")
+    m, k = x_q.shape
+    _require(a_scales.dim() == 1 and a_scales.dtype == torch.float32 and a_scales.numel() == m,
+             "a_scales must be 1D float32 with one value per input row")
+    n = _check_weight(qweight, w_scales, bias, k, out_dtype)
+    y = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if m == 0:
+        return y
+    with torch.cuda.device(dev):
+        rc = lib.tvq_w8a8_gemm(x_q.data_ptr(), a_scales.data_ptr(), qweight.data_ptr(), w_scales.data_ptr(),
+                               _ptr(bias), y.data_ptr(), _TORCH_TO_TVQ[out_dtype], m, n, k, _stream(dev))
+    _check(rc, "tvq_w8a8_gemm")
+    return y
+
+
+def w8a8_gemm_i32(x_q: torch.Tensor, qweight: torch.Tensor) -> torch.Tensor:
+    """The exact int32 accumulator x_q @ qweight^T of the W8A8 path."""
+    lib = load_library()
+    dev = _require_gpu(x_q, qweight)
+    _require(x_q.dim() == 2 and x_q.dtype == torch.int8, "x_q must be a 2-D int8 tensor")
+    _require(qweight.dim() == 2 and qweight.dtype == torch.int8, "qweight must be a 2-D int8 tensor")
+    m, k = x_q.shape
+    _require(qweight.shape[1] == k, "x_q and qweight shapes do not align")
+    n = qweight.shape[0]
+    y = torch.empty((m, n), dtype=torch.int32, device=dev)
+    if m == 0:
+        return y
+    with torch.cuda.device(dev):
+        rc = lib.tvq_w8a8_gemm_i32(x_q.data_ptr(), qweight.data_ptr(), y.data_ptr(), m, n, k, _stream(dev))
+    _check(rc, "tvq_w8a8_gemm_i32")
+    return y
+
+
+def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
+                bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused per-token activation quantization + W8A8 GEMM; output in x.dtype."""
+    lib = load_library()
+    dev = _require_gpu(x, qweight, w_scales, bias)
+    _require(x.dim() == 2, "x must be 2-D")
+    _require(x.dtype in _TORCH_TO_TVQ, "x must be float16 or bfloat16")
+    m, k = x.shape
+    n = _check_weight(qweight, w_scales, bias, k, x.dtype)
+    y = torch.empty((m, n), dtype=x.dtype, device=dev)
+    if m == 0:
+        return y
+    xq = torch.empty((m, k), dtype=torch.int8, device=dev)
+    a_s = torch.empty((m,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.tvq_w8a8_linear(x.data_ptr(), _TORCH_TO_TVQ[x.dtype], qweight.data_ptr(), w_scales.data_ptr(),
+                                 _ptr(bias), y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(), _stream(dev))
+    _check(rc, "tvq_w8a8_linear")
+    return y
