@@ -1,0 +1,379 @@
+"""Benchmark of the MI355X quantized-linear hot path.
+
+Default run (N=1): prints ONE JSON line for BASELINE.json's headline config
+(configs[1]): the W8A8 linear (per-token act-quant + int8 GEMM) at the
+Qwen3-0.6B QKV shape N=4096, K=1024, M=256. A "step" is one such linear over
+one batch of synthetic activations, using the next of a rotating pool of
+distinct weight copies (> 512 MB in total, i.e. larger than the 256 MB
+Infinity Cache, so weights come from HBM). Steps are captured in a HIP graph
+and replayed (the C ABI never allocates or syncs), so the timed region is GPU
+work, not Python launch overhead.
+
+Extra keys on the same line:
+  roofline      the dominant kernel (the W8A8 GEMM) timed with HIP events on
+                its launch stream: algorithmic bytes / average launch time
+  cpu_baseline  the reference's torch path (quantize -> dequantize -> F.linear)
+                restated in CPU torch, timed on this host's cores
+  sweep         configs 1-4: every (mode, shape, M) kernel with time, GB/s,
+                TOPS and roofline fraction (--quick skips it)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "tiny-vllm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+METRIC = "int8 GEMM TOPS & HBM GB/s (% roofline) at decode/prefill M; decode tok/s"
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+PEAK_I8_TOPS = 5000.0       # dense int8 MFMA, TOP/s
+PEAK_BF16_TFLOPS = 2500.0   # dense bf16 MFMA, TFLOP/s
+POOL_BYTES = 512 << 20      # rotating weight pool must exceed the 256 MB MALL
+
+HEADLINE = dict(name="qkv_0.6b", n=4096, k=1024, m=256)
+
+
+# ---------------------------------------------------------------- work formulas
+
+def w8a16_bytes(m, n, k):
+    return n * k + 4 * n + 2 * m * k + 2 * m * n
+
+
+def w8a8_gemm_bytes(m, n, k):
+    return n * k + 4 * n + m * k + 4 * m + 2 * m * n
+
+
+def act_quant_bytes(m, k):
+    return 3 * m * k + 4 * m
+
+
+def gemm_ops(m, n, k):
+    return 2 * m * n * k
+
+
+def roofline_for(mode, m, n, k, seconds):
+    ops = gemm_ops(m, n, k)
+    nbytes = w8a8_gemm_bytes(m, n, k) if mode == "w8a8" else w8a16_bytes(m, n, k)
+    peak_ops = PEAK_I8_TOPS if mode == "w8a8" else PEAK_BF16_TFLOPS
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    t_mfma = ops / (peak_ops * 1e12)
+    bound = "hbm" if t_hbm >= t_mfma else "mfma"
+    gbs = nbytes / seconds / 1e9
+    tops = ops / seconds / 1e12
+    frac = (t_hbm if bound == "hbm" else t_mfma) / seconds
+    return dict(bound=bound, gbs=gbs, tops=tops, frac=frac, bytes=nbytes, ops=ops)
+
+
+# ---------------------------------------------------------------- inputs
+
+def make_inputs(mode, m, n, k, dev, seed=0, pool_bytes=POOL_BYTES, max_copies=256):
+    """Activations (1% outlier columns x20 for W8A8) and a pool of weight copies,
+    generated on the GPU from a seeded device generator."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(m, k, generator=g, device=dev)
+    if mode == "w8a8":
+        cols = torch.randperm(k, generator=g, device=dev)[: max(1, k // 100)]
+        x[:, cols] *= 20.0
+    x = x.to(torch.bfloat16)
+    wbytes = n * k + 4 * n
+    copies = max(2, min(max_copies, math.ceil(pool_bytes / wbytes)))
+    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g, device=dev)
+    s = torch.rand(n, generator=g, device=dev) * 1e-3 + 1e-4
+    qs = [q] + [q.clone() for _ in range(copies - 1)]
+    ss = [s] + [s.clone() for _ in range(copies - 1)]
+    return x, qs, ss
+
+
+# ---------------------------------------------------------------- timing
+
+def _graph(fns):
+    """Capture the callables (each launches on the current stream) in a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in fns[: min(len(fns), 4)]:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, replays):
+    """Seconds per replay, HIP events on the current stream (the replay stream)."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / replays
+
+
+class Launcher:
+    """Pre-bound C-ABI launches with preallocated outputs (no allocation per call)."""
+
+    def __init__(self, lib, dev):
+        self.lib = lib
+        self.dev = dev
+
+    def stream(self):
+        return torch.cuda.current_stream(self.dev).cuda_stream
+
+    def act_quant(self, x, xq, a_s):
+        m, k = x.shape
+        return lambda: self._ck(self.lib.tvq_act_quant(x.data_ptr(), 1, m, k, 1e-8, xq.data_ptr(), a_s.data_ptr(),
+                                                       self.stream()))
+
+    def w8a8(self, xq, a_s, q, s, y):
+        m, k = xq.shape
+        n = q.shape[0]
+        return lambda: self._ck(self.lib.tvq_w8a8_gemm(xq.data_ptr(), a_s.data_ptr(), q.data_ptr(), s.data_ptr(),
+                                                       None, y.data_ptr(), 1, m, n, k, self.stream()))
+
+    def w8a8_linear(self, x, q, s, y, xq, a_s):
+        m, k = x.shape
+        n = q.shape[0]
+        return lambda: self._ck(self.lib.tvq_w8a8_linear(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None,
+                                                         y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(),
+                                                         self.stream()))
+
+    def w8a16(self, x, q, s, y):
+        m, k = x.shape
+        n = q.shape[0]
+        return lambda: self._ck(self.lib.tvq_w8a16_gemm(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None,
+                                                        y.data_ptr(), m, n, k, self.stream()))
+
+    def _ck(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.lib.tvq_last_error().decode())
+
+
+def time_kernel(make_fn, copies, min_launches=64, min_seconds=0.02):
+    """Average seconds per launch of a graph cycling over `copies` launch closures."""
+    fns = [make_fn(i) for i in range(copies)]
+    reps = max(1, math.ceil(min_launches / len(fns)))
+    fns = fns * reps
+    g = _graph(fns)
+    time_graph(g, 1)  # warm
+    per = time_graph(g, 1)
+    replays = max(1, math.ceil(min_seconds / max(per, 1e-9)))
+    return time_graph(g, replays) / len(fns)
+
+
+# ---------------------------------------------------------------- sweep (configs 1-4)
+
+def sweep_cases():
+    cases = []
+    cases.append(("cfg1", "w8a16", 64, 6144, 1024))                            # W8A16 gate_up 0.6B
+    for m in (1, 16, 64, 256, 512):                                            # cfg2 W8A8 QKV sweep
+        cases.append(("cfg2", "w8a8", m, 4096, 1024))
+    for name, n, k in (("down", 1024, 3072), ("o", 1024, 2048), ("gate_up", 6144, 1024)):  # cfg3 prefill
+        for mode in ("w8a8", "w8a16"):
+            cases.append((f"cfg3_{name}", mode, 8192, n, k))
+    big = (("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288))
+    for name, n, k in big:                                                    # cfg4 8B-like
+        for m in (1, 64, 512, 4096, 16384):
+            for mode in ("w8a16", "w8a8"):
+                cases.append((f"cfg4_{name}", mode, m, n, k))
+    return cases
+
+
+def run_sweep(lib, dev, quick=False):
+    from nanovllm.quantization import _hip
+    L = Launcher(lib, dev)
+    out = []
+    cases = sweep_cases()
+    if quick:
+        cases = [c for c in cases if c[0] in ("cfg1", "cfg2") or (c[0].startswith("cfg3") and c[1] == "w8a8")]
+    for tag, mode, m, n, k in cases:
+        x, qs, ss = make_inputs(mode, m, n, k, dev)
+        copies = len(qs)
+        if mode == "w8a8":
+            xq, a_s = _hip.act_quant(x)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            t = time_kernel(lambda i: L.w8a8(xq, a_s, qs[i], ss[i], y), copies)
+            xq2 = torch.empty_like(xq)
+            a_s2 = torch.empty_like(a_s)
+            tq = time_kernel(lambda i: L.act_quant(x, xq2, a_s2), 1)
+            path = _hip.select_path(_hip.OP_W8A8, m, n, k)
+        else:
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            t = time_kernel(lambda i: L.w8a16(x, qs[i], ss[i], y), copies)
+            tq = None
+            path = _hip.select_path(_hip.OP_W8A16, m, n, k)
+        r = roofline_for(mode, m, n, k, t)
+        rec = dict(cfg=tag, mode=mode, M=m, N=n, K=k, path=path, us=round(t * 1e6, 3), gbs=round(r["gbs"], 1),
+                   tops=round(r["tops"], 2), bound=r["bound"], frac=round(r["frac"], 4), weight_copies=copies)
+        if tq is not None:
+            rec["act_quant_us"] = round(tq * 1e6, 3)
+            rec["act_quant_gbs"] = round(act_quant_bytes(m, k) / tq / 1e9, 1)
+        out.append(rec)
+        print(json.dumps(rec), file=sys.stderr, flush=True)
+        del x, qs, ss, y
+        torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's torch path for the headline step on the host CPU:
+    quantize_int8_per_row_dynamic -> w8a8_linear_fallback (dequantize both
+    operands to bf16, F.linear), restated in oracle/ (utils.py:28-32,
+    cuda.py:455-465)."""
+    import oracle
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    m, n, k = HEADLINE["m"], HEADLINE["n"], HEADLINE["k"]
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g)
+    s = torch.rand(n, generator=g) * 1e-3 + 1e-4
+
+    def step():
+        xq, a_s = oracle.quantize_rows_torch(x)
+        return oracle.w8a8_torch_path(xq, a_s, q, s, None, torch.bfloat16)
+
+    for _ in range(2):
+        step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    nbytes = w8a8_gemm_bytes(m, n, k) + act_quant_bytes(m, k)
+    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                ms_per_step=round(med * 1e3, 3),
+                sample=f"{len(times)} steps of the headline W8A8 linear (M={m}, N={n}, K={k}), "
+                       f"median, torch CPU {torch.__version__} with {threads} threads, ~{budget_s:.0f}s budget")
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--quick", action="store_true", help="only configs 1-2 and W8A8 prefill in the sweep")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
+                         "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
+    args = ap.parse_args()
+    if args.profile:
+        args.no_sweep = args.no_cpu = True
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the quantized linear is a per-GPU kernel; sharding is a design note). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from nanovllm.quantization import _hip
+    lib = _hip.load_library()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    L = Launcher(lib, dev)
+
+    if args.profile:
+        # Calibration: a plain device copy of exactly 256 MiB in, 256 MiB out.
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    m, n, k = HEADLINE["m"], HEADLINE["n"], HEADLINE["k"]
+    x, qs, ss = make_inputs("w8a8", m, n, k, dev)
+    copies = len(qs)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    xq = torch.empty(m, k, dtype=torch.int8, device=dev)
+    a_s = torch.empty(m, dtype=torch.float32, device=dev)
+
+    # Headline: exactly `steps` W8A8 linears, graph-replayed, weights rotating.
+    g_warm = _graph([L.w8a8_linear(x, qs[i % copies], ss[i % copies], y, xq, a_s) for i in range(args.warmup)])
+    g_step = _graph([L.w8a8_linear(x, qs[i % copies], ss[i % copies], y, xq, a_s) for i in range(args.steps)])
+    g_warm.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    g_step.replay()
+    end.record()
+    torch.cuda.synchronize()
+    t_step = start.elapsed_time(end) / 1e3 / args.steps
+    step_bytes = w8a8_gemm_bytes(m, n, k) + act_quant_bytes(m, k)
+    value = step_bytes / t_step / 1e9
+
+    # Dominant kernel (the GEMM) on its own, same stream, HIP events.
+    xq0, a_s0 = _hip.act_quant(x)
+    t_gemm = time_kernel(lambda i: L.w8a8(xq0, a_s0, qs[i], ss[i], y), copies, min_launches=256)
+    r = roofline_for("w8a8", m, n, k, t_gemm)
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_w8a8_gemm_qkv_m256.json"
+    if tfile.is_file():
+        rec = json.loads(tfile.read_text())
+        if rec.get("kernel") == _hip.select_path(_hip.OP_W8A8, m, n, k):  # only for the kernel it measured
+            traffic = rec.get("hbm_bytes_per_launch")
+    roof = dict(bound=r["bound"], achieved=round(r["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(r["gbs"] / PEAK_HBM_GBS, 4), traffic=traffic,
+                kernel=_hip.select_path(_hip.OP_W8A8, m, n, k), kernel_us=round(t_gemm * 1e6, 3),
+                algorithmic_bytes=r["bytes"], tops=round(r["tops"], 3))
+    del x, qs, ss
+    torch.cuda.empty_cache()
+
+    sweep = None if args.no_sweep else run_sweep(lib, dev, quick=args.quick)
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations with 1% outlier columns x20; random int8 weights)",
+        "config": {
+            "workload": "W8A8 linear = per-token act-quant + int8 MFMA GEMM, Qwen3-0.6B qkv_proj "
+                        f"N={n} K={k}, M={m} tokens (BASELINE configs[1]); {copies} rotating weight copies "
+                        f"({copies * (n * k + 4 * n) / 2**20:.0f} MiB > MALL), HIP-graph replay",
+            "M": m, "N": n, "K": k, "out_dtype": "bf16",
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
