@@ -1,0 +1,206 @@
+"""CPU tests of the C ABI (no GPU compute) and of the Python dispatch layer.
+
+* the library loads and exports every symbol include/tvq.h declares;
+* argument validation and error reporting work without touching the GPU;
+* path selection is the documented M-bucketed table;
+* the nanovllm.quantization API keeps the reference's classes, parameter
+  names/dtypes/shapes, environment switches and log format
+  (nanovllm/quantization/{base,int8,w8a8,cuda}.py), and the torch path it
+  falls back to on request matches the oracle.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols() -> list[str]:
+    text = (ROOT / "include" / "tvq.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(tvq_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    syms = _declared_symbols()
+    for name in ("tvq_abi_version", "tvq_last_error", "tvq_select_path", "tvq_act_quant", "tvq_w8a16_gemm",
+                 "tvq_w8a8_gemm", "tvq_w8a8_gemm_i32", "tvq_w8a8_linear"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(hiplib):
+    from nanovllm.quantization import _hip
+    lib = ctypes.CDLL(str(_hip.library_path()))
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert {n for n, _, _ in _hip.SYMBOLS} == set(_declared_symbols())
+
+
+def test_abi_version_and_errors_without_gpu(hiplib):
+    assert hiplib.tvq_abi_version() == 1
+    assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None) == -1
+    assert b"dtype" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 1, 1, 16, None) == -1
+    assert b"null pointer" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a8_gemm(None, None, None, None, None, None, 1, 1, 0, 16, None) == -1
+    assert b"invalid shape" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a8_gemm_i32(None, None, None, 1, 1, 1 << 40, None) == -2
+    assert b"2^31" in hiplib.tvq_last_error()
+    assert hiplib.tvq_act_quant(None, 1, 4, 16, -1.0, None, None, None) == -1
+    # M == 0 is a valid no-op that launches nothing
+    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 0, 8, 16, None) == 0
+    assert hiplib.tvq_last_error() == b""
+
+
+def test_select_path_buckets(hiplib):
+    from nanovllm.quantization import _hip
+    sp = _hip.select_path
+    assert sp(_hip.OP_ACT_QUANT, 4, 0, 1024) == "act_quant_vec"
+    assert sp(_hip.OP_ACT_QUANT, 4, 0, 100) == "act_quant_scalar"
+    assert sp(_hip.OP_W8A16, 1, 4096, 1024).startswith("skinny_")
+    assert sp(_hip.OP_W8A16, 64, 4096, 1024).startswith("skinny_")
+    assert sp(_hip.OP_W8A8, 16, 4096, 1024).startswith("skinny_")
+    assert not sp(_hip.OP_W8A8, 8192, 1024, 3072).startswith("skinny_")
+    assert sp(_hip.OP_W8A8, 8, 33, 40) == "generic_simt"
+    with pytest.raises(RuntimeError):
+        sp(9, 1, 1, 1)
+
+
+# ------------------------------------------------------------------ Python API
+
+class _Layer(torch.nn.Module):
+    pass
+
+
+def test_quant_method_parameters_match_reference_layout():
+    from nanovllm.quantization import Int8WeightOnlyQuantMethod, W8A8QuantMethod
+    lay = _Layer()
+    Int8WeightOnlyQuantMethod().create_weights(lay, 1024, 4096)
+    assert lay.qweight.dtype == torch.int8 and tuple(lay.qweight.shape) == (4096, 1024)
+    assert lay.scales.dtype == torch.float32 and tuple(lay.scales.shape) == (4096,)
+    assert not lay.qweight.requires_grad and not lay.scales.requires_grad
+    assert Int8WeightOnlyQuantMethod().quantize_activation(torch.zeros(2, 4)) is None
+    lay2 = _Layer()
+    W8A8QuantMethod().create_weights(lay2, 3072, 1024)
+    assert lay2.qweight.dtype == torch.int8 and tuple(lay2.qweight.shape) == (1024, 3072)
+    assert lay2.w_scales.dtype == torch.float32 and tuple(lay2.w_scales.shape) == (1024,)
+    assert not hasattr(lay2, "scales")
+
+
+def _cpu_layer(method, n, k, seed=0):
+    x = torch.randn(3, 5, k, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(seed + 1)) * 0.02).to(torch.bfloat16)
+    q, s = oracle.quantize_rows(w.float().numpy())
+    lay = _Layer()
+    method.create_weights(lay, k, n)
+    lay.qweight.data.copy_(torch.from_numpy(q))
+    getattr(lay, "scales", getattr(lay, "w_scales", None)).data.copy_(torch.from_numpy(s))
+    lay.bias = None
+    return lay, x, torch.from_numpy(q), torch.from_numpy(s)
+
+
+def test_cpu_tensors_take_reference_torch_path_and_log(monkeypatch, capsys):
+    from nanovllm.quantization import Int8WeightOnlyQuantMethod, W8A8QuantMethod, cuda
+    monkeypatch.setenv("NANOVLLM_INT8_LOG_PATH", "1")
+    monkeypatch.setenv("NANOVLLM_W8A8_LOG_PATH", "1")
+    cuda._LOGGED_KERNEL_EVENTS.clear()
+    lay, x, q, s = _cpu_layer(Int8WeightOnlyQuantMethod(), 64, 128)
+    y = Int8WeightOnlyQuantMethod().apply(x, lay)
+    assert tuple(y.shape) == (3, 5, 64) and y.dtype == torch.bfloat16
+    assert torch.equal(y, oracle.w8a16_torch_path(x, q, s))
+    lay8, x8, q8, s8 = _cpu_layer(W8A8QuantMethod(), 64, 128, seed=3)
+    y8 = W8A8QuantMethod().apply(x8, lay8)
+    xq, a_s = oracle.quantize_rows_torch(x8.reshape(-1, 128))
+    ref = oracle.w8a8_torch_path(xq, a_s, q8, s8, None, torch.bfloat16).view(3, 5, 64)
+    assert torch.equal(y8, ref)
+    out = capsys.readouterr().out.strip().splitlines()
+    assert out[0].startswith("[nanovllm.int8] backend=fallback phase=decode path=python_fallback "
+                             "x_dtype=torch.bfloat16 x_shape=(3, 5, 128) qweight_shape=(64, 128)")
+    assert out[0].endswith("reason=cpu_tensors")
+    assert out[1].startswith("[nanovllm.w8a8] backend=fallback phase=decode path=python_fallback "
+                             "out_dtype=torch.bfloat16 x_q_shape=(15, 128) qweight_shape=(64, 128)")
+    # one-shot: the same event is not logged twice
+    Int8WeightOnlyQuantMethod().apply(x, lay)
+    assert capsys.readouterr().out == ""
+
+
+def test_backend_env_parsing(monkeypatch):
+    from nanovllm.quantization import cuda
+    for val, want in (("native", "native"), ("FALLBACK", "fallback"), (" cutlass ", "cutlass"), ("auto", "auto"),
+                      ("bogus", "native"), ("", "native")):
+        monkeypatch.setenv("NANOVLLM_INT8_BACKEND", val)
+        assert cuda._get_backend_preference() == want
+    for val, want in (("native", "native"), ("fallback", "fallback"), ("cutlass", "native")):
+        monkeypatch.setenv("NANOVLLM_W8A8_BACKEND", val)
+        assert cuda._get_w8a8_backend_preference() == want
+    for val, want in (("", False), ("0", False), ("off", False), ("1", True), ("yes", True)):
+        monkeypatch.setenv("NANOVLLM_INT8_LOG_PATH", val)
+        assert cuda._should_log_kernel_path() is want
+
+
+def test_forced_fallback_logs_reason(monkeypatch, capsys):
+    from nanovllm.quantization import cuda
+    monkeypatch.setenv("NANOVLLM_INT8_BACKEND", "fallback")
+    monkeypatch.setenv("NANOVLLM_INT8_LOG_PATH", "1")
+    cuda._LOGGED_KERNEL_EVENTS.clear()
+    from nanovllm.utils.context import reset_context, set_context
+    set_context(True)
+    try:
+        lay, x, q, s = _cpu_layer(__import__("nanovllm.quantization", fromlist=["x"]).Int8WeightOnlyQuantMethod(),
+                                  32, 64)
+        cuda.apply_int8_weight_only_linear(x, lay.qweight, lay.scales)
+    finally:
+        reset_context()
+    line = capsys.readouterr().out.strip()
+    assert "backend=fallback phase=prefill path=python_fallback" in line
+    assert line.endswith("reason=backend_forced_fallback")
+
+
+def test_native_entry_points_refuse_cpu_tensors():
+    """The native path never silently computes on the CPU."""
+    from nanovllm.quantization import cuda
+    lay, x, q, s = _cpu_layer(__import__("nanovllm.quantization", fromlist=["x"]).Int8WeightOnlyQuantMethod(), 32, 64)
+    with pytest.raises(RuntimeError):
+        cuda.native_int8_weight_only_linear(x, q, s)
+    xq, a_s = oracle.quantize_rows_torch(x.reshape(-1, 64))
+    with pytest.raises(RuntimeError):
+        cuda.native_w8a8_linear(xq, a_s, q, s, None, torch.bfloat16)
+
+
+def test_validation_messages_match_reference():
+    from nanovllm.quantization import cuda
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    q = torch.zeros(8, 32, dtype=torch.int8)
+    s = torch.zeros(8)
+    with pytest.raises(RuntimeError, match="Incompatible shapes"):
+        cuda.native_int8_weight_only_linear(x, q, s)
+    with pytest.raises(RuntimeError, match="scales must be 1D"):
+        cuda.native_int8_weight_only_linear(x[:, :32], q, torch.zeros(7))
+    with pytest.raises(RuntimeError, match="bias must be 1D"):
+        cuda.native_int8_weight_only_linear(x[:, :32], q, s, torch.zeros(3))
+    xq = torch.zeros(2, 32, dtype=torch.int8)
+    with pytest.raises(RuntimeError, match="a_scales must be 1D"):
+        cuda.native_w8a8_linear(xq, torch.zeros(3), q, s, None, torch.bfloat16)
+    with pytest.raises(RuntimeError, match="output dtype"):
+        cuda.native_w8a8_linear(xq, torch.zeros(2), q, s, None, torch.float32)
+
+
+def test_utils_quantizers_match_oracle():
+    from nanovllm.quantization.utils import (is_qwen3_int8_target_weight, quantize_int8_per_channel,
+                                             quantize_int8_per_row_dynamic)
+    w = (torch.randn(64, 256, generator=torch.Generator().manual_seed(1)) * 0.02).to(torch.bfloat16)
+    q, s = quantize_int8_per_channel(w)
+    q_o, s_o = oracle.quantize_rows(w.float().numpy())
+    np.testing.assert_array_equal(q.numpy(), q_o)
+    np.testing.assert_array_equal(s.numpy(), s_o)
+    q2, s2 = quantize_int8_per_row_dynamic(w)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    assert is_qwen3_int8_target_weight("model.layers.0.mlp.down_proj.weight")
+    assert not is_qwen3_int8_target_weight("model.layers.0.input_layernorm.weight")

@@ -226,6 +226,41 @@ def test_prefill_full_size_sampled_rows(hiplib, mode, nk):
     assert (y[-100:].float() == 0).all()
 
 
+# (M, N, K) hitting every DMA tile configuration with ragged M and N edges.
+DMA_RAGGED = [("w8a8", 4100, 8200, 1024), ("w8a8", 4000, 1700, 1024), ("w8a8", 700, 1000, 1152),
+              ("w8a8", 200, 3000, 1024), ("w8a16", 3000, 3300, 1024), ("w8a16", 700, 1000, 1152),
+              ("w8a16", 100, 2050, 2048)]
+
+
+@pytest.mark.parametrize("case", DMA_RAGGED, ids=lambda c: "-".join(map(str, c)))
+def test_dma_ragged_sampled_rows(hiplib, case):
+    """Every DMA tile configuration with M and N not multiples of the tile:
+    sampled rows (always including the last) checked exactly (W8A8) or within
+    the bound (W8A16), plus the last output column of every row."""
+    from nanovllm.quantization import _hip
+    mode, m, n, k = case
+    op = _hip.OP_W8A8 if mode == "w8a8" else _hip.OP_W8A16
+    _log_case(test="dma_ragged", mode=mode, m=m, n=n, k=k, path=_hip.select_path(op, m, n, k))
+    assert _hip.select_path(op, m, n, k).startswith("dma_")
+    d = _dev()
+    x = make_activations(m, k, seed=m + n, outlier_frac=0.01 if mode == "w8a8" else 0.0)
+    q, s = make_weights(n, k, seed=n + k)
+    rows = np.unique(np.concatenate([np.random.default_rng(m).choice(m, 24, replace=False), [0, m - 1]]))
+    xr = x[torch.from_numpy(rows)]
+    if mode == "w8a8":
+        y = _hip.w8a8_linear(x.to(d), q.to(d), s.to(d))
+        xq, a_s = oracle.c_act_quant(bits16(xr))
+        yb_ref, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq, q.numpy()), a_s, s.numpy())
+        np.testing.assert_array_equal(bits16(y)[rows], yb_ref)
+        xq_all, a_all = oracle.c_act_quant(bits16(x))
+        col, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq_all, q.numpy()[-1:]), a_all, s.numpy()[-1:])
+        np.testing.assert_array_equal(bits16(y)[:, -1:], col)
+    else:
+        y = _hip.w8a16_gemm(x.to(d), q.to(d), s.to(d))
+        _w8a16_check(y.cpu()[torch.from_numpy(rows)], xr, q, s)
+        _w8a16_check(y.cpu()[:, -1:], x, q[-1:], s[-1:])
+
+
 # ---------------------------------------------------------------- graph capture
 
 def test_hip_graph_capture_replay(hiplib):

@@ -43,7 +43,7 @@ def test_quant_single_nonzero_maps_to_127():
 def test_quant_amax_element_is_127_for_all_magnitudes():
     rng = np.random.default_rng(0)
     for _ in range(200):
-        x = rng.standard_normal((1, 64)).astype(np.float32) * np.float32(10.0 ** rng.uniform(-20, 20))
+        x = rng.standard_normal((1, 64)).astype(np.float32) * np.float32(10.0 ** rng.uniform(-4, 20))  # amax/127 stays above eps
         q, _ = oracle.quantize_rows(x)
         i = np.argmax(np.abs(x[0]))
         assert abs(int(q[0, i])) == 127
@@ -84,9 +84,10 @@ def test_quant_eps_floor():
     q, s = oracle.quantize_rows(x)
     assert s[0] == np.float32(1e-8)
     assert q[0].tolist() == [0, 0, 0]
-    x = np.array([[1e-6 * 127 / 128, 0.5e-8]], np.float32)  # amax/127 just under 1e-8? no: check both sides
-    q, s = oracle.quantize_rows(x)
-    assert s[0] == max(np.float32(x[0, 0]) / np.float32(127.0), np.float32(1e-8))
+    for amax in (1.26e-6, 1.28e-6):  # amax/127 just below and just above eps
+        x = np.array([[amax, 0.5e-8]], np.float32)
+        q, s = oracle.quantize_rows(x)
+        assert s[0] == max(np.float32(amax) / np.float32(127.0), np.float32(1e-8))
 
 
 def test_quant_matches_brute_force_python():

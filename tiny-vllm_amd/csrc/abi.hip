@@ -57,6 +57,7 @@ int run_gemm(const GemmArgs& a, void* stream) {
   switch (select_gemm_path(a)) {
     case Path::kSkinny: e = launch_skinny(a, (hipStream_t)stream); break;
     case Path::kTiled: e = launch_tiled(a, (hipStream_t)stream); break;
+    case Path::kDma: e = launch_dma_gemm(a, (hipStream_t)stream); break;
     default: e = launch_generic(a, (hipStream_t)stream); break;
   }
   if (e != hipSuccess) return fail(TVQ_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
@@ -68,11 +69,11 @@ int run_gemm(const GemmArgs& a, void* stream) {
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
   if (!aligned) return Path::kGeneric;
-  return a.M <= kSkinnyMaxM ? Path::kSkinny : Path::kTiled;
+  if (a.M <= kSkinnyMaxM) return Path::kSkinny;
+  return dma_shape_ok(a.K) ? Path::kDma : Path::kTiled;
 }
 
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
-  (void)N;
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
   if (M <= kSkinnyMaxM) {
     static const char* names8[4] = {"skinny_mfma_i8_m16", "skinny_mfma_i8_m32", "skinny_mfma_i8_m48",
@@ -82,6 +83,7 @@ const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool alig
     const int mg = M <= 0 ? 0 : (int)((M + 15) / 16) - 1;
     return w8a8 ? names8[mg] : names16[mg];
   }
+  if (dma_shape_ok(K)) return dma_path_name(w8a8, M, N);
   return w8a8 ? "tiled_mfma_i8_128x128x128" : "tiled_mfma_f16x_128x128x64";
 }
 

@@ -1,0 +1,419 @@
+// Multi-stage LDS-DMA pipelined W8A16 / W8A8 GEMM for gfx950 (kernel template).
+//
+// Operands are moved global -> LDS with global_load_lds_dwordx4 (no register
+// staging) into an S-deep ring of stages; each stage covers 128 k values, so
+// S-1 stages of loads are in flight while the MFMAs of the current one run.
+//
+// One wave-level DMA fills one 1 KB block: 8 rows x 128 contiguous bytes of
+// the operand (full cache lines). Lane i fetches row i/8, 16-byte chunk
+// c = (i%8) ^ (i/8) of that row, and the hardware writes it to block + 16*i;
+// so chunk c of row rho sits in slot rho*8 + (c ^ rho). The XOR spreads the
+// 16 rows a fragment read touches across all LDS banks (no conflicts) while
+// every DMA still reads whole 128-byte lines.
+//
+// Fragment reads (one ds_read_b128 per lane, lane = 16*g + r):
+//   weight / int8 activation, 64-k sub-step ks: row r, chunk 4*ks + g
+//     (k = 64*ks + 16g .. +16)
+//   16-bit activation (two blocks per 8 rows: k 0-63 and 64-127), sub-step
+//     ks, half b: row r, chunk 2g + b of block ks (k = 64*ks + 16g + 8b .. +8)
+// For W8A16 the 16 int8 weights of a lane (k = 16g..16g+15) are converted to
+// two 8-element bf16/fp16 halves; half b pairs with activation half b, which
+// holds the same 8 k values. Any consistent k assignment gives the same dot
+// product.
+//
+// Output channels are the MFMA A side, so each lane owns y[m, n..n+3].
+//
+// Row indices past M or N are clamped to the last row: those rows only feed
+// output rows/columns that are never stored. K must be a multiple of 128
+// (checked by the dispatcher), so no K tail is read.
+//
+// Waits are explicit: the compiler does not track LDS-DMA completion, so each
+// step waits on vmcnt for its own stage and then crosses an s_barrier (a bare
+// barrier, without the workgroup fence that would force vmcnt(0)).
+#pragma once
+
+#include <type_traits>
+
+#include "tvq_common.h"
+
+namespace tvq {
+namespace dma {
+
+#define TVQ_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
+#define TVQ_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Wait until at most `ahead` later stages (each `LPW` DMA ops) are in flight.
+template <int LPW, int S>
+__device__ __forceinline__ void wait_stage(int ahead) {
+  static_assert(LPW * (S - 2) < 64, "too many DMA ops in flight for vmcnt");
+  if constexpr (S >= 5) {
+    if (ahead >= 3) { wait_vm<LPW * 3>(); return; }
+  }
+  if constexpr (S >= 4) {
+    if (ahead >= 2) { wait_vm<LPW * 2>(); return; }
+  }
+  if constexpr (S >= 3) {
+    if (ahead >= 1) { wait_vm<LPW>(); return; }
+  }
+  wait_vm<0>();
+}
+
+template <bool kW8A8, int BM, int BN, int WM, int WN, int S, int MF>
+struct Cfg {
+  static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kXHalves = kW8A8 ? 1 : 2;          // 128-byte segments per activation row per stage
+  static constexpr int kWBlk = BN / 8;                    // weight blocks per stage
+  static constexpr int kXBlk = (BM / 8) * kXHalves;       // activation blocks per stage
+  static constexpr int kBlkStage = kWBlk + kXBlk;
+  static constexpr int kStageBytes = kBlkStage * 1024;
+  static constexpr int kLdsBytes = kStageBytes * S;
+  static constexpr int kLPW = kBlkStage / kWaves;         // DMA ops per wave per stage
+  static constexpr int kKStage = 128;                     // k values per stage
+  static constexpr int TM = BM / WM, TN = BN / WN;
+  static constexpr int FM = TM / MF, FN = TN / MF;        // MFMA tiles per wave
+  static_assert(MF == 16 || MF == 32, "MFMA tile is 16x16 or 32x32");
+  static_assert(kBlkStage % kWaves == 0, "stage blocks must split evenly over waves");
+  static_assert(TM % MF == 0 && TN % MF == 0, "wave tile must be a multiple of the MFMA tile");
+  static_assert(S >= 2, "at least double buffering");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+// Store four consecutive outputs y[m, nb..nb+3] with the path's epilogue.
+template <typename T, bool kW8A8, bool kRaw, typename V>
+__device__ __forceinline__ void store4(void* yv, const float* ws, const uint16_t* bias, float as, int m, int nb, int N,
+                                       V v0, V v1, V v2, V v3) {
+  if constexpr (kRaw) {
+    int32_t* y = static_cast<int32_t*>(yv) + (int64_t)m * N;
+    const int32_t v[4] = {(int32_t)v0, (int32_t)v1, (int32_t)v2, (int32_t)v3};
+    if (nb + 3 < N && (N & 3) == 0) {
+      *reinterpret_cast<i32x4*>(y + nb) = i32x4{v[0], v[1], v[2], v[3]};
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (nb + t < N) y[nb + t] = v[t];
+    }
+  } else {
+    uint16_t* y = static_cast<uint16_t*>(yv) + (int64_t)m * N;
+    const V v[4] = {v0, v1, v2, v3};
+    float o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int n = nb + t < N ? nb + t : N - 1;
+      const float bb = bias ? to_float<T>(bias[n]) : 0.0f;
+      if constexpr (kW8A8)
+        o[t] = epi_w8a8(v[t], as, ws[n], bb);
+      else
+        o[t] = epi_w8a16(v[t], ws[n], bb);
+    }
+    if (nb + 3 < N && (N & 3) == 0) {
+      u32x2 pk;
+      pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
+      pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
+      *reinterpret_cast<u32x2*>(y + nb) = pk;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (nb + t < N) y[nb + t] = from_float<T>(o[t]);
+    }
+  }
+}
+
+// Offset (bytes) of 16-byte chunk `c` of row `row` inside a run of 8-row
+// blocks laid out by the DMA (chunk c of row rho at slot rho*8 + (c ^ rho)).
+__device__ __forceinline__ int chunk_off(int row, int c) {
+  const int rho = row & 7;
+  return (row >> 3) * 1024 + 16 * (rho * 8 + (c ^ rho));
+}
+
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
+                                                                const float* __restrict__ a_scales,
+                                                                const int8_t* __restrict__ qw,
+                                                                const float* __restrict__ ws,
+                                                                const uint16_t* __restrict__ bias,
+                                                                void* __restrict__ yv, int M, int N, int K,
+                                                                int group, int m_major) {
+  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
+  using Acc = typename std::conditional<
+      MF == 32, typename std::conditional<kW8A8, i32x16, f32x16>::type,
+      typename std::conditional<kW8A8, i32x4, f32x4>::type>::type;
+  constexpr int kAccN = MF == 32 ? 16 : 4;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wn = wave % WN;
+  const int wm = wave / WN;
+
+  // ---- tile order: XCD chunking, then grouped swizzle -------------------
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int total = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
+  int tm, tn;
+  if (m_major) {
+    // consecutive tiles walk m inside groups of `group` n-tiles
+    const int per_group = group * tiles_m;
+    const int first = (pid / per_group) * group;
+    const int gsz = min(tiles_n - first, group);
+    const int in = pid % per_group;
+    tn = first + in % gsz;
+    tm = in / gsz;
+  } else {
+    // consecutive tiles walk n inside groups of `group` m-tiles
+    const int per_group = group * tiles_n;
+    const int first = (pid / per_group) * group;
+    const int gsz = min(tiles_m - first, group);
+    const int in = pid % per_group;
+    tm = first + in % gsz;
+    tn = in / gsz;
+  }
+  const int n0 = tn * BN;
+  const int m0 = tm * BM;
+
+  // ---- per-lane DMA sources for this wave's blocks ----------------------
+  const char* src[C::kLPW];
+  int ldsoff[C::kLPW];
+  int stride[C::kLPW];
+  {
+    const int rho = lane >> 3;           // row within the 8-row block
+    const int chunk = (lane & 7) ^ rho;  // 16-byte chunk this lane fetches
+#pragma unroll
+    for (int j = 0; j < C::kLPW; ++j) {
+      const int b = j * C::kWaves + wave;
+      ldsoff[j] = b * 1024;
+      if (b < C::kWBlk) {
+        const int n = min(n0 + 8 * b + rho, N - 1);
+        src[j] = reinterpret_cast<const char*>(qw) + (int64_t)n * K + 16 * chunk;
+        stride[j] = C::kKStage;
+      } else {
+        const int xb = b - C::kWBlk;
+        const int m = min(m0 + 8 * (xb / C::kXHalves) + rho, M - 1);
+        const int half = xb % C::kXHalves;
+        src[j] = static_cast<const char*>(xv) + (int64_t)m * K * (kW8A8 ? 1 : 2) + 128 * half + 16 * chunk;
+        stride[j] = kW8A8 ? C::kKStage : 2 * C::kKStage;
+      }
+    }
+  }
+
+  auto issue = [&](int kt) {
+    char* stage = smem + (kt % S) * C::kStageBytes;
+#pragma unroll
+    for (int j = 0; j < C::kLPW; ++j)
+      __builtin_amdgcn_global_load_lds(TVQ_GPTR(src[j] + (int64_t)kt * stride[j]), TVQ_LPTR(stage + ldsoff[j]), 16, 0,
+                                       0);
+  };
+
+  // ---- lane-constant fragment offsets within a stage ---------------------
+  // MF = 16: lane = 16*g + r, sub-steps of 64 k (2 per stage).
+  // MF = 32: lane = 32*h + r, sub-steps of 32 k (4 per stage).
+  constexpr int kSub = MF == 32 ? 4 : 2;
+  constexpr int kRows = MF;                        // rows per fragment
+  const int r = lane % MF;
+  const int g = lane / MF;                         // lane group: 0..3 (MF 16) or 0..1 (MF 32)
+  int woff[kSub];        // weight / int8 activation fragment
+  int xoff[kSub][2];     // 16-bit activation fragment, halves b = 0, 1
+#pragma unroll
+  for (int ks = 0; ks < kSub; ++ks) {
+    // 16 bytes per lane: k = ks*(128/kSub) + 16*g .. +16
+    const int c = ks * (8 / kSub) + g;
+    woff[ks] = chunk_off(r, c);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      // 16-bit activations: k = ks*(128/kSub) + 16*g + 8*b .. +8, two 64-k halves per row
+      const int k = ks * (128 / kSub) + 16 * g + 8 * b;
+      const int rho = r & 7;
+      xoff[ks][b] = (r >> 3) * 2048 + (k >> 6) * 1024 + 16 * (rho * 8 + (((k & 63) >> 3) ^ rho));
+    }
+  }
+  constexpr int kWFrag = kRows / 8 * 1024;         // bytes per weight fragment (rows x 128 B)
+  constexpr int kXFrag = kW8A8 ? kWFrag : 2 * kWFrag;
+
+  Acc acc[C::FN][C::FM];
+#pragma unroll
+  for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
+
+  const int nk = K / C::kKStage;
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_stage<C::kLPW, S>(min(S - 2, nk - 1 - kt));
+    barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1);
+
+    const char* wst = smem + (kt % S) * C::kStageBytes + wn * C::FN * kWFrag;
+    const char* xst = smem + (kt % S) * C::kStageBytes + C::kWBlk * 1024 + wm * C::FM * kXFrag;
+    // Fragments are double-buffered in registers: the LDS reads of sub-step
+    // ks+1 are issued before the MFMAs of sub-step ks, so their latency hides
+    // behind the matrix core instead of stalling the wave.
+    u32x4 fa[2][C::FN];
+    u32x4 fb[2][C::FM][kW8A8 ? 1 : 2];
+    auto load_frags = [&](int ks, int buf) {
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(wst + i * kWFrag + woff[ks]);
+#pragma unroll
+      for (int j = 0; j < C::FM; ++j) {
+        if constexpr (kW8A8) {
+          fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + woff[ks]);
+        } else {
+          fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][0]);
+          fb[buf][j][1] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][1]);
+        }
+      }
+    };
+    load_frags(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < kSub; ++ks) {
+      const int cb = ks & 1;
+      if (ks + 1 < kSub) load_frags(ks + 1, cb ^ 1);
+      // Keep the scheduler from sinking those reads below this sub-step's MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kW8A8) {
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) {
+#pragma unroll
+          for (int i = 0; i < C::FN; ++i) {
+            if constexpr (MF == 32)
+              acc[i][j] = mfma32x32x32_i8(fa[cb][i], fb[cb][j][0], acc[i][j]);
+            else
+              acc[i][j] = mfma16x16x64_i8(fa[cb][i], fb[cb][j][0], acc[i][j]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) {
+          const u32x2 c0 = i8x4_to_16x4<T>(fa[cb][i][0]);
+          const u32x2 c1 = i8x4_to_16x4<T>(fa[cb][i][1]);
+          const u32x2 c2 = i8x4_to_16x4<T>(fa[cb][i][2]);
+          const u32x2 c3 = i8x4_to_16x4<T>(fa[cb][i][3]);
+          const u32x4 alo = u32x4{c0.x, c0.y, c1.x, c1.y};
+          const u32x4 ahi = u32x4{c2.x, c2.y, c3.x, c3.y};
+#pragma unroll
+          for (int j = 0; j < C::FM; ++j) {
+            if constexpr (MF == 32) {
+              acc[i][j] = mfma32x32x16<T>(alo, fb[cb][j][0], acc[i][j]);
+              acc[i][j] = mfma32x32x16<T>(ahi, fb[cb][j][1], acc[i][j]);
+            } else {
+              acc[i][j] = mfma16x16x32<T>(alo, fb[cb][j][0], acc[i][j]);
+              acc[i][j] = mfma16x16x32<T>(ahi, fb[cb][j][1], acc[i][j]);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue -----------------------------------------------------------
+  // MF 16: acc reg t -> n = 4g + t.  MF 32: reg v -> n = 8*(v/4) + 4g + v%4.
+  // Either way a lane owns runs of 4 consecutive output channels of token r.
+  if constexpr (kRaw) {
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j) {
+      const int m = m0 + wm * C::TM + MF * j + r;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i) {
+        const Acc v = acc[i][j];
+#pragma unroll
+        for (int q = 0; q < kAccN / 4; ++q) {
+          const int nb = n0 + wn * C::TN + MF * i + 8 * q + 4 * g;
+          store4<T, kW8A8, kRaw>(yv, ws, bias, 0.0f, m, nb, N, v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        }
+      }
+    }
+  } else {
+    // Stage the finished 16-bit tile in LDS (the operand ring is free now),
+    // then write whole rows with coalesced 16-byte stores. Row m of the tile
+    // is 2*BN bytes; its 16-byte chunks are XOR-swizzled by (m & 15) so the
+    // 4-element writes of 16+ different rows land on different banks.
+    static_assert(BM * BN * 2 <= C::kLdsBytes, "output tile must fit in the LDS ring");
+    constexpr int kChunks = BN / 8;
+    constexpr int kSwz = (kChunks < 16 ? kChunks : 16) - 1;
+    __syncthreads();
+    auto toff = [&](int ml, int nl) { return ml * (2 * BN) + 16 * ((nl >> 3) ^ (ml & kSwz)) + 2 * (nl & 7); };
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j) {
+      const int ml = wm * C::TM + MF * j + r;
+      const int m = min(m0 + ml, M - 1);
+      float as = 0.0f;
+      if constexpr (kW8A8) as = a_scales[m];
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i) {
+        const Acc v = acc[i][j];
+#pragma unroll
+        for (int q = 0; q < kAccN / 4; ++q) {
+          const int nl = wn * C::TN + MF * i + 8 * q + 4 * g;
+          float o[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int n = min(n0 + nl + t, N - 1);
+            const float bb = bias ? to_float<T>(bias[n]) : 0.0f;
+            if constexpr (kW8A8)
+              o[t] = epi_w8a8(v[4 * q + t], as, ws[n], bb);
+            else
+              o[t] = epi_w8a16(v[4 * q + t], ws[n], bb);
+          }
+          u32x2 pk;
+          pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
+          pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
+          *reinterpret_cast<u32x2*>(smem + toff(ml, nl)) = pk;
+        }
+      }
+    }
+    __syncthreads();
+    const bool vec = (N & 7) == 0;
+    uint16_t* y = static_cast<uint16_t*>(yv);
+    for (int c = threadIdx.x; c < BM * kChunks; c += C::kThreads) {
+      const int ml = c / kChunks;
+      const int cl = c % kChunks;
+      const int m = m0 + ml;
+      const int n = n0 + 8 * cl;
+      if (m >= M || n >= N) continue;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(smem + ml * (2 * BN) + 16 * (cl ^ (ml & kSwz)));
+      uint16_t* dst = y + (int64_t)m * N + n;
+      if (vec && n + 8 <= N) {
+        *reinterpret_cast<u32x4*>(dst) = val;
+      } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(&val);
+        for (int t = 0; t < 8 && n + t < N; ++t) dst[t] = h[t];
+      }
+    }
+  }
+}
+
+// Host-side launcher for one configuration.
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF>
+hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
+                      int M, int N, int K, int group, int m_major, hipStream_t stream) {
+  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF>;
+  static bool attr_set = false;  // idempotent; a benign race sets it twice
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  kern<<<dim3(tiles), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias),
+                                                                  y, M, N, K, group, m_major);
+  return hipGetLastError();
+}
+
+}  // namespace dma
+}  // namespace tvq

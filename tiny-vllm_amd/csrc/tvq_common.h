@@ -43,6 +43,11 @@ __device__ __forceinline__ uint16_t from_float<BF16>(float f) {
 }
 template <>
 __device__ __forceinline__ uint16_t from_float<F16>(float f) {
+  // Pin the fp32 value first: otherwise the compiler may fuse the producing
+  // multiply into a mixed-precision fma (v_fma_mix*) that rounds once,
+  // straight to fp16, instead of rounding to fp32 and then to fp16 as the
+  // reference does (static_cast<at::Half>(float)).
+  asm("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
@@ -87,6 +92,26 @@ __device__ __forceinline__ f32x4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, f32x4 c) {
 template <>
 __device__ __forceinline__ f32x4 mfma16x16x32<F16>(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// One 32x32x16 MFMA on 16-bit operands (eight elements per lane).
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32x32x16<BF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32x32x16<F16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// One 32x32x32 int8 MFMA with exact int32 accumulation.
+__device__ __forceinline__ i32x16 mfma32x32x32_i8(u32x4 a, u32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
 // One 16x16x64 int8 MFMA with exact int32 accumulation.

@@ -10,7 +10,8 @@ namespace tvq {
 enum class Path : int {
   kGeneric = 0,  // scalar reference-order kernel: any K, any alignment
   kSkinny = 1,   // M <= 64: weight-streaming MFMA GEMV / skinny GEMM
-  kTiled = 2,    // M > 64: LDS double-buffered MFMA tiles
+  kTiled = 2,    // M > 64, K % 128 != 0: register-staged double-buffered MFMA tiles
+  kDma = 3,      // M > 64, K % 128 == 0: LDS-DMA multi-stage MFMA tiles
 };
 
 struct GemmArgs {
@@ -37,6 +38,9 @@ const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool alig
 hipError_t launch_skinny(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_tiled(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_generic(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream);
+bool dma_shape_ok(int64_t K);
+const char* dma_path_name(bool w8a8, int64_t M, int64_t N);
 
 // Largest M served by the skinny family.
 constexpr int64_t kSkinnyMaxM = 64;
