@@ -64,10 +64,17 @@ def test_select_path_buckets(hiplib):
     sp = _hip.select_path
     assert sp(_hip.OP_ACT_QUANT, 4, 0, 1024) == "act_quant_vec"
     assert sp(_hip.OP_ACT_QUANT, 4, 0, 100) == "act_quant_scalar"
-    assert sp(_hip.OP_W8A16, 1, 4096, 1024).startswith("skinny_")
-    assert sp(_hip.OP_W8A16, 64, 4096, 1024).startswith("skinny_")
-    assert sp(_hip.OP_W8A8, 16, 4096, 1024).startswith("skinny_")
-    assert not sp(_hip.OP_W8A8, 8192, 1024, 3072).startswith("skinny_")
+    assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "skinny_mfma_f16x_m16"
+    assert sp(_hip.OP_W8A16, 64, 4096, 1024) == "skinny_mfma_f16x_m64"
+    assert sp(_hip.OP_W8A8, 16, 24576, 4096) == "stream_mfma_i8_m16"    # wide N, M > 8
+    assert sp(_hip.OP_W8A16, 64, 24576, 4096) == "stream_mfma_f16x_m64"
+    assert sp(_hip.OP_W8A8, 8, 24576, 4096) == "skinny_mfma_i8_m16"     # M <= 8
+    assert sp(_hip.OP_W8A8, 16, 24576, 4160) == "skinny_mfma_i8_m16"    # K % 256 != 0
+    assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_32x64"
+    assert sp(_hip.OP_W8A8, 8192, 1024, 3072) == "dma_mfma_i8_256x128"
+    assert sp(_hip.OP_W8A8, 8192, 6144, 1024) == "dma_mfma_i8_256x256"
+    assert sp(_hip.OP_W8A16, 8192, 1024, 3072) == "dma_mfma_f16x_128x256"
+    assert sp(_hip.OP_W8A8, 300, 1000, 1040).startswith("tiled_")         # K % 128 != 0
     assert sp(_hip.OP_W8A8, 8, 33, 40) == "generic_simt"
     with pytest.raises(RuntimeError):
         sp(9, 1, 1, 1)

@@ -58,6 +58,7 @@ int run_gemm(const GemmArgs& a, void* stream) {
     case Path::kSkinny: e = launch_skinny(a, (hipStream_t)stream); break;
     case Path::kTiled: e = launch_tiled(a, (hipStream_t)stream); break;
     case Path::kDma: e = launch_dma_gemm(a, (hipStream_t)stream); break;
+    case Path::kStream: e = launch_stream(a, (hipStream_t)stream); break;
     default: e = launch_generic(a, (hipStream_t)stream); break;
   }
   if (e != hipSuccess) return fail(TVQ_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
@@ -69,12 +70,19 @@ int run_gemm(const GemmArgs& a, void* stream) {
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
   if (!aligned) return Path::kGeneric;
-  if (a.M <= kSkinnyMaxM) return Path::kSkinny;
+  if (a.M <= kSkinnyMaxM) return stream_shape_ok(a.M, a.N, a.K) ? Path::kStream : Path::kSkinny;
   return dma_shape_ok(a.K) ? Path::kDma : Path::kTiled;
 }
 
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
+  if (M <= kSkinnyMaxM && stream_shape_ok(M, N, K)) {
+    static const char* s8[4] = {"stream_mfma_i8_m16", "stream_mfma_i8_m32", "stream_mfma_i8_m48", "stream_mfma_i8_m64"};
+    static const char* s16[4] = {"stream_mfma_f16x_m16", "stream_mfma_f16x_m32", "stream_mfma_f16x_m48",
+                                 "stream_mfma_f16x_m64"};
+    const int mg = (int)((M + 15) / 16) - 1;
+    return w8a8 ? s8[mg] : s16[mg];
+  }
   if (M <= kSkinnyMaxM) {
     static const char* names8[4] = {"skinny_mfma_i8_m16", "skinny_mfma_i8_m32", "skinny_mfma_i8_m48",
                                     "skinny_mfma_i8_m64"};

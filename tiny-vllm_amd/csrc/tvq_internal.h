@@ -12,6 +12,7 @@ enum class Path : int {
   kSkinny = 1,   // M <= 64: weight-streaming MFMA GEMV / skinny GEMM
   kTiled = 2,    // M > 64, K % 128 != 0: register-staged double-buffered MFMA tiles
   kDma = 3,      // M > 64, K % 128 == 0: LDS-DMA multi-stage MFMA tiles
+  kStream = 4,   // 8 < M <= 64, N >= 16384, K % 256 == 0: weight streaming, LDS-shared activations
 };
 
 struct GemmArgs {
@@ -42,7 +43,10 @@ hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream);
 bool dma_shape_ok(int64_t K);
 const char* dma_path_name(bool w8a8, int64_t M, int64_t N);
 
-// Largest M served by the skinny family.
+hipError_t launch_stream(const GemmArgs& a, hipStream_t stream);
+bool stream_shape_ok(int64_t M, int64_t N, int64_t K);
+
+// Largest M served by the skinny / stream families.
 constexpr int64_t kSkinnyMaxM = 64;
 
 }  // namespace tvq
