@@ -139,6 +139,30 @@ def w8a8_torch_path(x_q, a_scales, qweight, w_scales, bias=None, out_dtype=None)
     return F.linear(x, weight, bias)
 
 
+def w8a16_fp32_scale_torch(x, qweight, scales, bias=None):
+    """The GPU kernels' W8A16 numerics in torch: fp32 sum of x * int8 (exact
+    products), per-channel fp32 scale and bias once per output, one rounding
+    to x.dtype. Differs from the reference torch path only in not rounding
+    the dequantized weight to bf16 (int8_weight_only_gemm.cu:397-413 rounds)."""
+    import torch
+    y = (x.float() @ qweight.float().T) * scales.float()[None, :]
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(x.dtype)
+
+
+def w8a8_fp32_scale_torch(x_q, a_scales, qweight, w_scales, bias=None, out_dtype=None):
+    """The GPU kernels' W8A8 numerics in torch: exact integer accumulator,
+    (float(acc) * a_s) * w_s + b in fp32 (w8a8_gemm.cu:387-390 order), one
+    rounding to the output dtype."""
+    import torch
+    acc = (x_q.to(torch.int64) @ qweight.to(torch.int64).T).float()
+    y = acc * a_scales.float()[:, None] * w_scales.float()[None, :]
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(out_dtype or torch.bfloat16)
+
+
 def quantize_rows_torch(x):
     """quantize_int8_per_row_dynamic (utils.py:28-32) in CPU torch."""
     import torch

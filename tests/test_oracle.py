@@ -278,6 +278,24 @@ def test_w8a8_torch_path_close_to_exact():
     assert oracle.rel_l2(oracle.bf16_bits_to_f32(yb), y64) <= oracle.rel_l2(f32(y), y64)
 
 
+def test_fp32_scale_torch_models_match_exact_and_c_epilogue():
+    """The model-level helpers restating the kernels' fp32-scale numerics:
+    W8A8 equals the C epilogue up to the unfused bias-free fma (<= 1 bf16 ulp
+    on ties of the two roundings); W8A16 is within fp32 summation error of
+    the fp64 product."""
+    x = make_activations(16, 512, seed=15)
+    xq, a_s = oracle.quantize_rows(f32(x))
+    q, w_s = make_weights(96, 512, seed=16)
+    y = oracle.w8a8_fp32_scale_torch(torch.from_numpy(xq), torch.from_numpy(a_s), q, w_s, None, torch.bfloat16)
+    yb, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq, q.numpy()), a_s, w_s.numpy())
+    got, ref = f32(y), oracle.bf16_bits_to_f32(yb)
+    assert np.mean(got == ref) > 0.999
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7)
+    y16 = oracle.w8a16_fp32_scale_torch(x, q, w_s)
+    y64 = oracle.w8a16_f64(f32(x), q.numpy(), w_s.numpy())
+    assert np.all(np.abs(f32(y16) - y64) <= np.abs(y64) * 2.0 ** -8 + 1e-6 * np.abs(y64).max())
+
+
 # ------------------------------------------------------------ golden fixtures
 
 def _golden_files():

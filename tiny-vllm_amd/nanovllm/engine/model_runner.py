@@ -1,0 +1,142 @@
+"""Runs one engine step on the GPU (reference: nanovllm/engine/model_runner.py).
+
+Owns the model, the KV cache and the sampler:
+  * the model is built on cuda:0 in bf16. Weights come from `config.model`'s
+    safetensors (or `quantized_model_path` for an "int8" / "w8a8" artifact)
+    when present; otherwise every parameter is drawn at random
+    (projections ~N(0, 0.02), norms 1) from a seeded generator in a fixed
+    order, so a bf16 and a quantized engine built with the same seed hold the
+    same weights up to quantization (the quantized layers store
+    quantize_int8_per_channel of the bf16 draw);
+  * KV cache: one tensor [2, layers, slots, kv_heads, max_model_len, head_dim]
+    whose per-layer views go to each Attention; one slot per running sequence;
+  * sampling: argmax where temperature == 0, otherwise the reference's
+    exponential-race sampler (softmax(logits / T) / Exp(1), argmax).
+"""
+from __future__ import annotations
+
+import os
+from glob import glob
+
+import torch
+from torch import nn
+
+from nanovllm.config import Config
+from nanovllm.engine.sequence import Sequence
+from nanovllm.layers.linear import LinearBase
+from nanovllm.models.qwen3 import Attention, Qwen3ForCausalLM, RMSNorm
+from nanovllm.quantization.utils import quantize_int8_per_channel
+from nanovllm.utils.context import reset_context, set_context
+from nanovllm.utils.loader import load_model
+
+
+def sample(logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Tensor:
+    """Greedy rows (T == 0) take argmax; the rest follow reference sampler.py:10-15."""
+    greedy = logits.argmax(dim=-1)
+    if bool((temperatures > 0).any()):
+        t = torch.where(temperatures > 0, temperatures, torch.ones_like(temperatures))
+        probs = torch.softmax(logits.float() / t[:, None], dim=-1)
+        drawn = probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
+        return torch.where(temperatures > 0, drawn, greedy)
+    return greedy
+
+
+@torch.no_grad()
+def random_init_(model: nn.Module, seed: int, std: float = 0.02, device: str = "cuda") -> None:
+    """Seeded random weights in module order; quantized linears store the
+    per-channel int8 quantization of the same bf16 draw."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for mod in model.modules():
+        if isinstance(mod, LinearBase):
+            n, k = (mod.weight if mod.quant_method is None else mod.qweight).shape
+            w = torch.empty(n, k, device=device, dtype=torch.bfloat16).normal_(0.0, std, generator=gen)
+            if mod.quant_method is None:
+                mod.weight.copy_(w)
+            else:
+                q, s = quantize_int8_per_channel(w)
+                mod.qweight.copy_(q)
+                getattr(mod, "scales", getattr(mod, "w_scales", None)).copy_(s)
+            if mod.bias is not None:
+                mod.bias.zero_()
+        elif isinstance(mod, RMSNorm):
+            mod.weight.fill_(1.0)
+        elif isinstance(mod, nn.Embedding):
+            mod.weight.normal_(0.0, std, generator=gen)
+        elif isinstance(mod, nn.Linear) and mod.weight is not getattr(model, "model").embed_tokens.weight:
+            mod.weight.normal_(0.0, std, generator=gen)
+
+
+class ModelRunner:
+    def __init__(self, config: Config, device: str = "cuda"):
+        # device="cpu" exists for host-only tests of the engine logic; the
+        # quantized layers then take the reference's torch path.
+        if device == "cuda":
+            if not torch.cuda.is_available():
+                raise RuntimeError("the engine needs a GPU (cuda:0)")
+            torch.cuda.set_device(0)
+        self.config = config
+        self.device = device
+        hf = config.hf_config
+        default_dtype = torch.get_default_dtype()
+        torch.set_default_dtype(torch.bfloat16)
+        with torch.device(device):
+            self.model = Qwen3ForCausalLM(hf, config.quantization)
+        torch.set_default_dtype(default_dtype)
+        has_weights = isinstance(config.model, str) and glob(os.path.join(config.model, "*.safetensors"))
+        if config.quantization and config.quantized_model_path:
+            load_model(self.model, config.quantized_model_path, config.quantization)
+        elif has_weights and not config.quantization:
+            load_model(self.model, config.model)
+        else:
+            random_init_(self.model, config.seed, device=device)
+        self.model.eval()
+        self._allocate_kv_cache()
+
+    def _allocate_kv_cache(self) -> None:
+        cfg, hf = self.config, self.config.hf_config
+        attns = [m for m in self.model.modules() if isinstance(m, Attention)]
+        per_slot = 2 * len(attns) * attns[0].num_kv_heads * cfg.max_model_len * hf.head_dim * 2
+        if self.device == "cuda":
+            free, _ = torch.cuda.mem_get_info()
+            budget = int(free * cfg.gpu_memory_utilization)
+        else:
+            budget = 1 << 30
+        self.num_slots = min(cfg.max_num_seqs, budget // per_slot)
+        if self.num_slots < 1:
+            raise RuntimeError(f"not enough GPU memory for one KV slot of {cfg.max_model_len} tokens")
+        # Zero-filled once: masked positions still enter p @ V with weight 0,
+        # so the cache must never hold non-finite values.
+        self.kv_cache = torch.zeros(2, len(attns), self.num_slots, attns[0].num_kv_heads, cfg.max_model_len,
+                                    hf.head_dim, dtype=torch.bfloat16, device=self.device)
+        for i, a in enumerate(attns):
+            a.k_cache, a.v_cache = self.kv_cache[0, i], self.kv_cache[1, i]
+
+    def _to_gpu(self, values, dtype) -> torch.Tensor:
+        if self.device == "cpu":
+            return torch.tensor(values, dtype=dtype)
+        return torch.tensor(values, dtype=dtype, pin_memory=True).cuda(non_blocking=True)
+
+    @torch.no_grad()
+    def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
+        if is_prefill:
+            ids, pos, cu = [], [], [0]
+            for s in seqs:
+                ids.extend(s.token_ids)
+                pos.extend(range(len(s)))
+                cu.append(cu[-1] + len(s))
+            set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=max(len(s) for s in seqs),
+                        slot_mapping=torch.tensor([s.slot for s in seqs]))
+            hidden = self.model(self._to_gpu(ids, torch.int64), self._to_gpu(pos, torch.int64))
+            hidden = hidden[self._to_gpu(cu[1:], torch.int64) - 1]
+        else:
+            slots = [s.slot for s in seqs]
+            lens = [len(s) for s in seqs]
+            set_context(False, max_seqlen_k=max(lens), slot_mapping=self._to_gpu(slots, torch.int64),
+                        context_lens=self._to_gpu(lens, torch.int64), kv_lo=min(slots), kv_hi=max(slots) + 1)
+            hidden = self.model(self._to_gpu([s.last_token for s in seqs], torch.int64),
+                                self._to_gpu([n - 1 for n in lens], torch.int64))
+        logits = self.model.compute_logits(hidden)
+        temps = self._to_gpu([s.temperature for s in seqs], torch.float32)
+        tokens = sample(logits, temps).tolist()
+        reset_context()
+        return tokens

@@ -18,6 +18,8 @@ class Context:
     slot_mapping: torch.Tensor | None = None
     context_lens: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
+    kv_lo: int = 0   # decode: KV-cache slot range of the running batch
+    kv_hi: int = 0
 
 
 _CONTEXT = Context()
@@ -28,10 +30,10 @@ def get_context() -> Context:
 
 
 def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0, slot_mapping=None,
-                context_lens=None, block_tables=None) -> None:
+                context_lens=None, block_tables=None, kv_lo=0, kv_hi=0) -> None:
     global _CONTEXT
     _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, slot_mapping,
-                       context_lens, block_tables)
+                       context_lens, block_tables, kv_lo, kv_hi)
 
 
 def reset_context() -> None:
