@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define TVQ_ABI_VERSION 1
+#define TVQ_ABI_VERSION 2
 
 /* Activation / output element types. */
 enum tvq_dtype {
@@ -116,6 +116,30 @@ int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight,
                     const float* w_scales, const void* bias, void* y,
                     int64_t M, int64_t N, int64_t K, int8_t* xq_buf,
                     float* a_scales_buf, void* stream);
+
+/* Fused RMSNorm producer of a projection input. Replaces RMSNorm.rms_forward
+ * / add_rms_forward (nanovllm/layers/layernorm.py:16-40), optionally followed
+ * by quantize_int8_per_row_dynamic (nanovllm/quantization/utils.py:28-32) of
+ * its output, as W8A8QuantMethod.quantize_activation (w8a8.py:21-23) would
+ * apply it in the next qkv_proj / gate_up_proj. Per row of K elements:
+ *   h = x (+ residual);  residual <- h  (in place, when residual != NULL)
+ *   y = (h * rsqrt(mean(h^2) + eps)) * weight   (rounded as torch rounds)
+ * and, when xq != NULL, xq / a_scales = per-token int8 codes and scale of y,
+ * bit-identical to tvq_act_quant(y). y and xq may each be NULL (not both).
+ * x, residual, weight and y have `dtype`; weight is [K]. No buffer may alias
+ * another. */
+int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps,
+                void* y, int8_t* xq, float* a_scales, int dtype, int64_t M,
+                int64_t K, void* stream);
+
+/* Fused SiLU-and-multiply producer of the down_proj input. Replaces
+ * SiluAndMul.forward (nanovllm/layers/activation.py:11-14) on gate_up
+ * [M, 2*I] (gate = columns [0, I), up = [I, 2I)): y = silu(gate) * up,
+ * [M, I], optionally followed by the per-token int8 quantization of y as in
+ * tvq_rmsnorm (xq / a_scales bit-identical to tvq_act_quant(y)). y and xq
+ * may each be NULL (not both). */
+int tvq_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales,
+                 int dtype, int64_t M, int64_t I, void* stream);
 
 #ifdef __cplusplus
 }

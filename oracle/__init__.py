@@ -163,6 +163,36 @@ def w8a8_fp32_scale_torch(x_q, a_scales, qweight, w_scales, bias=None, out_dtype
     return y.to(out_dtype or torch.bfloat16)
 
 
+def rmsnorm_ref(x_f32: np.ndarray, w_f32: np.ndarray, eps: float, res_f32: np.ndarray | None = None,
+                is_bf16: bool = True):
+    """RMSNorm of layernorm.py:16-40 with its roundings, statistics in fp64.
+    x, w, residual are the (exactly representable) fp32 values of bf16/fp16
+    inputs. Returns (y, new_residual or None) as fp32 arrays of rounded values:
+      h = fp32(x + res)  (one fp32 rounding, as torch's fp32 add)
+      r = 1/sqrt(mean(h^2) + eps)  (fp64 here; fp32 on the device)
+      y = rnd(fp32(rnd(fp32(h*r)) * w))"""
+    rnd = (lambda a: bf16_bits_to_f32(f32_to_bf16_bits(a))) if is_bf16 else \
+        (lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32))
+    h = np.asarray(x_f32, np.float32)
+    new_res = None
+    if res_f32 is not None:
+        h = (h + np.asarray(res_f32, np.float32)).astype(np.float32)
+        new_res = rnd(h)
+    hd = h.astype(np.float64)
+    r = 1.0 / np.sqrt((hd * hd).mean(axis=-1, keepdims=True) + eps)
+    y1 = rnd((hd * r).astype(np.float32))
+    y = rnd((y1 * np.asarray(w_f32, np.float32)).astype(np.float32))
+    return y, new_res
+
+
+def silu_mul_ref(gu_f32: np.ndarray, is_bf16: bool = True) -> np.ndarray:
+    """SiluAndMul (activation.py:11-14) in fp64, one rounding to bf16/fp16."""
+    rnd = (lambda a: bf16_bits_to_f32(f32_to_bf16_bits(a))) if is_bf16 else \
+        (lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32))
+    g, u = np.split(np.asarray(gu_f32, np.float64), 2, axis=-1)
+    return rnd((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+
+
 def quantize_rows_torch(x):
     """quantize_int8_per_row_dynamic (utils.py:28-32) in CPU torch."""
     import torch

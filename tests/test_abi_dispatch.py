@@ -31,7 +31,7 @@ def _declared_symbols() -> list[str]:
 def test_header_declares_expected_entry_points():
     syms = _declared_symbols()
     for name in ("tvq_abi_version", "tvq_last_error", "tvq_select_path", "tvq_act_quant", "tvq_w8a16_gemm",
-                 "tvq_w8a8_gemm", "tvq_w8a8_gemm_i32", "tvq_w8a8_linear"):
+                 "tvq_w8a8_gemm", "tvq_w8a8_gemm_i32", "tvq_w8a8_linear", "tvq_rmsnorm", "tvq_silu_mul"):
         assert name in syms
 
 
@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol(hiplib):
 
 
 def test_abi_version_and_errors_without_gpu(hiplib):
-    assert hiplib.tvq_abi_version() == 1
+    assert hiplib.tvq_abi_version() == 2
     assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None) == -1
     assert b"dtype" in hiplib.tvq_last_error()
     assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 1, 1, 16, None) == -1
@@ -54,6 +54,13 @@ def test_abi_version_and_errors_without_gpu(hiplib):
     assert hiplib.tvq_w8a8_gemm_i32(None, None, None, 1, 1, 1 << 40, None) == -2
     assert b"2^31" in hiplib.tvq_last_error()
     assert hiplib.tvq_act_quant(None, 1, 4, 16, -1.0, None, None, None) == -1
+    assert hiplib.tvq_rmsnorm(None, None, None, 1e-6, None, None, None, 1, 4, 16, None) == -1
+    assert b"null pointer" in hiplib.tvq_last_error()
+    assert hiplib.tvq_rmsnorm(1, None, 1, 1e-6, None, None, None, 1, 4, 16, None) == -1
+    assert b"needs an output" in hiplib.tvq_last_error()
+    assert hiplib.tvq_silu_mul(1, None, 1, None, 1, 4, 16, None) == -1
+    assert b"without a_scales" in hiplib.tvq_last_error()
+    assert hiplib.tvq_silu_mul(1, 1, None, None, 1, 0, 16, None) == 0
     # M == 0 is a valid no-op that launches nothing
     assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 0, 8, 16, None) == 0
     assert hiplib.tvq_last_error() == b""

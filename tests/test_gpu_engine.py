@@ -50,14 +50,19 @@ def _rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
 @pytest.mark.parametrize("mode", ["int8", "w8a8"])
 def test_quantized_projections_run_native(gpu, hiplib, monkeypatch, mode):
     calls = {"n": 0}
-    name = "w8a16_gemm" if mode == "int8" else "w8a8_linear"
-    orig = getattr(_hip, name)
+    # W8A16: every projection is one tvq_w8a16_gemm. W8A8: o_proj quantizes its
+    # input itself (tvq_w8a8_linear); qkv / gate_up / down receive int8 codes
+    # from the fused norm / SiLU producers (tvq_w8a8_gemm).
+    names = ["w8a16_gemm"] if mode == "int8" else ["w8a8_linear", "w8a8_gemm"]
 
-    def counted(*a, **k):
-        calls["n"] += 1
-        return orig(*a, **k)
+    def counting(orig):
+        def counted(*a, **k):
+            calls["n"] += 1
+            return orig(*a, **k)
+        return counted
 
-    monkeypatch.setattr(_hip, name, counted)
+    for name in names:
+        monkeypatch.setattr(_hip, name, counting(getattr(_hip, name)))
     llm = _engine(mode)
     llm.generate([[1, 2, 3, 4, 5, 6]], SamplingParams(temperature=0.0, max_tokens=3, ignore_eos=True),
                  use_tqdm=False)
@@ -74,15 +79,22 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
     fp32-scale numerics."""
     import oracle
     from nanovllm.layers.linear import LinearBase
+    from nanovllm.quantization.activation import QuantizedActivation
     llm = _engine(mode)
     model = llm.model_runner.model
     seen = []
-    hooks = [m.register_forward_hook(lambda mod, inp, out: seen.append((mod, inp[0].detach().cpu(), out.detach().cpu())))
-             for m in model.modules() if isinstance(m, LinearBase)]
+    def grab(mod, inp, out):
+        x = inp[0]
+        x = QuantizedActivation(x.xq.cpu(), x.scales.cpu(), x.dtype, x.shape) \
+            if isinstance(x, QuantizedActivation) else x.detach().cpu()
+        seen.append((mod, x, out.detach().cpu()))
+
+    hooks = [m.register_forward_hook(grab) for m in model.modules() if isinstance(m, LinearBase)]
     _prefill_logits(model, list(range(7, 7 + 200, 3)) + [5] * 31, "cuda")
     for h in hooks:
         h.remove()
     assert len(seen) == 4 * SMALL["num_hidden_layers"]
+    fused = 0
     for mod, x, y in seen:
         q = mod.qweight.cpu()
         if mode == "int8":
@@ -91,9 +103,13 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
             ref_own = oracle.w8a16_fp32_scale_torch(x, q, s)
         else:
             s = mod.w_scales.cpu()
-            xq, a_s = oracle.quantize_rows_torch(x)
-            gq, ga = _hip.act_quant(x.cuda())
-            assert torch.equal(gq.cpu(), xq) and torch.equal(ga.cpu(), a_s)
+            if isinstance(x, QuantizedActivation):   # codes from a fused producer
+                xq, a_s = x.xq, x.scales
+                fused += 1
+            else:
+                xq, a_s = oracle.quantize_rows_torch(x)
+                gq, ga = _hip.act_quant(x.cuda())
+                assert torch.equal(gq.cpu(), xq) and torch.equal(ga.cpu(), a_s)
             ref_path = oracle.w8a8_torch_path(xq, a_s, q, s, None, torch.bfloat16)
             ref_own = oracle.w8a8_fp32_scale_torch(xq, a_s, q, s, None, torch.bfloat16)
         yf = y.float().numpy()
@@ -103,6 +119,7 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
             assert oracle.max_abs_ratio(yf, rf) <= oracle.MAX_ABS_TOL
         # against its own numerics the kernel is far tighter than the tolerance
         assert oracle.rel_l2(yf, ref_own.float().numpy()) < 2e-3
+    assert fused == (3 * SMALL["num_hidden_layers"] if mode == "w8a8" else 0)
 
 
 def test_bf16_kv_cache_decode_matches_recompute(gpu):

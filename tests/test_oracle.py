@@ -296,6 +296,45 @@ def test_fp32_scale_torch_models_match_exact_and_c_epilogue():
     assert np.all(np.abs(f32(y16) - y64) <= np.abs(y64) * 2.0 ** -8 + 1e-6 * np.abs(y64).max())
 
 
+# ------------------------------------------------------------ producers
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rmsnorm_ref_matches_reference_torch_expression(dtype):
+    """oracle.rmsnorm_ref against the reference's torch ops (layernorm.py:16-40)
+    run by CPU torch: residual bit-exact, y within one ulp (fp64 vs fp32
+    statistics), almost all bit-exact; plus closed-form special cases."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(64, 1024, generator=g).to(dtype)
+    r = torch.randn(64, 1024, generator=g).to(dtype)
+    w = (torch.rand(1024, generator=g) + 0.5).to(dtype)
+    h = x.float() + r.float()
+    res_t = h.to(dtype)
+    y_t = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype) * w
+    y, res = oracle.rmsnorm_ref(f32(x), f32(w), 1e-6, f32(r), is_bf16=dtype == torch.bfloat16)
+    np.testing.assert_array_equal(res, f32(res_t))
+    assert np.mean(y == f32(y_t)) > 0.999
+    # a constant row c normalises to sign(c) (eps negligible): y = w exactly
+    yc, _ = oracle.rmsnorm_ref(np.full((1, 64), 3.0, np.float32), np.full(64, 0.75, np.float32), 0.0)
+    assert np.all(yc == 0.75)
+    # zero row -> zeros
+    yz, _ = oracle.rmsnorm_ref(np.zeros((1, 16), np.float32), np.ones(16, np.float32), 1e-6)
+    assert np.all(yz == 0)
+
+
+def test_silu_mul_ref_matches_torch_and_closed_forms():
+    g = torch.Generator().manual_seed(22)
+    gu = (torch.randn(32, 2048, generator=g) * 3).bfloat16()
+    a, b = gu.float().chunk(2, -1)
+    y_t = (torch.nn.functional.silu(a) * b).bfloat16()
+    y = oracle.silu_mul_ref(f32(gu))
+    assert np.mean(y == f32(y_t)) > 0.999
+    # gate | up = [0, ln 3 | 5, 1]: silu(0) * 5 = 0; silu(ln 3) * 1 = ln3 / (1 + 1/3) = 0.75 ln 3
+    v = np.array([[0.0, np.log(3.0), 5.0, 1.0]], np.float32)
+    out = oracle.silu_mul_ref(v)
+    assert out[0, 0] == 0.0
+    assert out[0, 1] == oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(np.float32(0.75 * np.log(3.0))))
+
+
 # ------------------------------------------------------------ golden fixtures
 
 def _golden_files():

@@ -167,4 +167,32 @@ int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight, const float
   return tvq_w8a8_gemm(xq_buf, a_scales_buf, qweight, w_scales, bias, y, dtype, M, N, K, stream);
 }
 
+int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps, void* y, int8_t* xq, float* a_scales,
+                int dtype, int64_t M, int64_t K, void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dims(M, 1, K)) return rc;
+  if (M == 0) return ok();
+  if (!x || !weight) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (!y && !xq) return fail(TVQ_E_INVALID, "rmsnorm needs an output: y and/or xq");
+  if (xq && !a_scales) return fail(TVQ_E_INVALID, "xq given without a_scales");
+  if (!(eps >= 0.0f)) return fail(TVQ_E_INVALID, "eps must be >= 0");
+  hipError_t e = launch_rmsnorm(x, residual, weight, eps, y, xq, a_scales, dtype == TVQ_DTYPE_BF16, M, K,
+                                (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "rmsnorm launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int tvq_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales, int dtype, int64_t M, int64_t I,
+                 void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dims(M, 1, 2 * I)) return rc;
+  if (M == 0) return ok();
+  if (!gate_up) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (!y && !xq) return fail(TVQ_E_INVALID, "silu_mul needs an output: y and/or xq");
+  if (xq && !a_scales) return fail(TVQ_E_INVALID, "xq given without a_scales");
+  hipError_t e = launch_silu_mul(gate_up, y, xq, a_scales, dtype == TVQ_DTYPE_BF16, M, I, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "silu_mul launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -29,6 +29,10 @@ struct GemmArgs {
 };
 
 bool act_quant_vec_ok(const void* x, const void* xq, int64_t K);
+hipError_t launch_rmsnorm(const void* x, void* residual, const void* weight, float eps, void* y, int8_t* xq,
+                          float* a_scales, bool bf16, int64_t M, int64_t K, hipStream_t stream);
+hipError_t launch_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales, bool bf16, int64_t M,
+                           int64_t I, hipStream_t stream);
 hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
                             hipStream_t stream);
 

@@ -4,11 +4,12 @@
 Every qkv / o / gate_up / down projection is a tensor-parallel Linear from
 nanovllm.layers.linear, so with `quantization` = "int8" or "w8a8" the 4
 projections of each layer run on the gfx950 quantized kernels (112 linears
-for the 28-layer 0.6B model). Everything else is plain PyTorch:
-RMSNorm (fp32 statistics, fused residual add), per-head q/k RMSNorm, rotary
-embedding (rotate-half, neox style), grouped-query attention over the
-engine's KV cache (SDPA for prefill, batched matmuls for decode),
-SiLU(gate) * up, tied or separate LM head.
+for the 28-layer 0.6B model). RMSNorm (with the fused residual add) and
+SiLU-and-multiply run on the fused HIP producer kernels, which for W8A8 also
+emit the next projection's int8 codes and per-token scales. The rest is plain
+PyTorch: rotary embedding (rotate-half, neox style), grouped-query attention
+over the engine's KV cache (SDPA for prefill, batched matmuls for decode),
+tied or separate LM head.
 
 Attention reads its per-step metadata from nanovllm.utils.context, which the
 engine sets before each forward:
@@ -24,6 +25,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from nanovllm.layers.activation import SiluAndMul
+from nanovllm.layers.layernorm import RMSNorm
 from nanovllm.layers.linear import MergedColumnParallelLinear, QKVParallelLinear, RowParallelLinear
 from nanovllm.utils.context import get_context
 
@@ -44,24 +47,6 @@ class Qwen3Config:
     tie_word_embeddings: bool = True
     attention_bias: bool = False
     hidden_act: str = "silu"
-
-
-class RMSNorm(nn.Module):
-    def __init__(self, hidden_size: int, eps: float = 1e-6):
-        super().__init__()
-        self.eps = eps
-        self.weight = nn.Parameter(torch.ones(hidden_size))
-
-    def _norm(self, x: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        return xf.to(x.dtype) * self.weight
-
-    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):
-        if residual is None:
-            return self._norm(x)
-        summed = (x.float() + residual.float()).to(x.dtype)
-        return self._norm(summed), summed
 
 
 class RotaryEmbedding(nn.Module):
@@ -179,10 +164,11 @@ class Qwen3MLP(nn.Module):
         self.gate_up_proj = MergedColumnParallelLinear(cfg.hidden_size, [cfg.intermediate_size] * 2,
                                                        quantization=quantization)
         self.down_proj = RowParallelLinear(cfg.intermediate_size, cfg.hidden_size, quantization=quantization)
+        self.act_fn = SiluAndMul()
+        self.fuse_quant = quantization == "w8a8"
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, up = self.gate_up_proj(x).chunk(2, dim=-1)
-        return self.down_proj((F.silu(gate) * up).contiguous())
+    def forward(self, x) -> torch.Tensor:
+        return self.down_proj(self.act_fn(self.gate_up_proj(x), quant=self.fuse_quant))
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -192,14 +178,18 @@ class Qwen3DecoderLayer(nn.Module):
         self.mlp = Qwen3MLP(cfg, quantization)
         self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        # W8A8: the norms emit int8 codes + per-token scales for qkv_proj and
+        # gate_up_proj directly (fused producer quantization).
+        self.fuse_quant = quantization == "w8a8"
 
     def forward(self, positions, h, residual):
+        q = self.fuse_quant
         if residual is None:
-            h, residual = self.input_layernorm(h), h
+            h, residual = self.input_layernorm(h, quant=q), h
         else:
-            h, residual = self.input_layernorm(h, residual)
+            h, residual = self.input_layernorm(h, residual, quant=q)
         h = self.self_attn(positions, h)
-        h, residual = self.post_attention_layernorm(h, residual)
+        h, residual = self.post_attention_layernorm(h, residual, quant=q)
         return self.mlp(h), residual
 
 

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_NAME = "libtinyvllm_quant.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OP_ACT_QUANT = 0
 OP_W8A16 = 1
@@ -41,6 +41,8 @@ SYMBOLS = (
     ("tvq_w8a8_gemm", _INT, (_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP)),
     ("tvq_w8a8_gemm_i32", _INT, (_VP, _VP, _VP, _I64, _I64, _I64, _VP)),
     ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP)),
+    ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
+    ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
 )
 
 
@@ -241,3 +243,55 @@ def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
                                  _ptr(bias), y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(), _stream(dev))
     _check(rc, "tvq_w8a8_linear")
     return y
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+            out: bool = True, quant: bool = False):
+    """RMSNorm of each row of x (after adding `residual`, which is then
+    updated in place to the sum), on the GPU. Returns (y or None,
+    (xq, a_scales) or None): y in x.dtype when `out`, the per-token int8
+    codes and scales of y when `quant`."""
+    lib = load_library()
+    dev = _require_gpu(x, weight, residual)
+    _require(x.dim() == 2 and x.is_contiguous(), "x must be a contiguous 2-D tensor")
+    _require(x.dtype in _TORCH_TO_TVQ, "x must be float16 or bfloat16")
+    _require(out or quant, "rmsnorm needs an output")
+    m, k = x.shape
+    _require(weight.dim() == 1 and weight.numel() == k and weight.dtype == x.dtype and weight.is_contiguous(),
+             "weight must be a contiguous 1-D tensor of x's dtype and length K")
+    if residual is not None:
+        _require(residual.shape == x.shape and residual.dtype == x.dtype and residual.is_contiguous(),
+                 "residual must match x")
+    y = torch.empty_like(x) if out else None
+    q = (torch.empty((m, k), dtype=torch.int8, device=dev), torch.empty((m,), dtype=torch.float32, device=dev)) \
+        if quant else None
+    if m == 0:
+        return y, q
+    with torch.cuda.device(dev):
+        rc = lib.tvq_rmsnorm(x.data_ptr(), _ptr(residual), weight.data_ptr(), eps, _ptr(y),
+                             q[0].data_ptr() if q else None, q[1].data_ptr() if q else None,
+                             _TORCH_TO_TVQ[x.dtype], m, k, _stream(dev))
+    _check(rc, "tvq_rmsnorm")
+    return y, q
+
+
+def silu_mul(gate_up: torch.Tensor, out: bool = True, quant: bool = False):
+    """silu(gate_up[:, :I]) * gate_up[:, I:] on the GPU. Returns (y or None,
+    (xq, a_scales) or None) as rmsnorm."""
+    lib = load_library()
+    dev = _require_gpu(gate_up)
+    _require(gate_up.dim() == 2 and gate_up.is_contiguous(), "gate_up must be a contiguous 2-D tensor")
+    _require(gate_up.dtype in _TORCH_TO_TVQ, "gate_up must be float16 or bfloat16")
+    _require(gate_up.shape[1] % 2 == 0, "gate_up must have an even number of columns")
+    _require(out or quant, "silu_mul needs an output")
+    m, i = gate_up.shape[0], gate_up.shape[1] // 2
+    y = torch.empty((m, i), dtype=gate_up.dtype, device=dev) if out else None
+    q = (torch.empty((m, i), dtype=torch.int8, device=dev), torch.empty((m,), dtype=torch.float32, device=dev)) \
+        if quant else None
+    if m == 0:
+        return y, q
+    with torch.cuda.device(dev):
+        rc = lib.tvq_silu_mul(gate_up.data_ptr(), _ptr(y), q[0].data_ptr() if q else None,
+                              q[1].data_ptr() if q else None, _TORCH_TO_TVQ[gate_up.dtype], m, i, _stream(dev))
+    _check(rc, "tvq_silu_mul")
+    return y, q

@@ -4,6 +4,7 @@ import torch
 from torch import nn
 
 from nanovllm.quantization import _hip
+from nanovllm.quantization.activation import QuantizedActivation
 from nanovllm.quantization.base import QuantMethod
 from nanovllm.quantization.cuda import _get_w8a8_backend_preference, apply_w8a8_linear, native_w8a8_fused_linear
 from nanovllm.quantization.utils import quantize_int8_per_row_dynamic
@@ -32,6 +33,10 @@ class W8A8QuantMethod(QuantMethod):
 
     def apply(self, x: torch.Tensor, layer: nn.Module, bias: torch.Tensor | None = None) -> torch.Tensor:
         bias = bias if bias is not None else layer.bias
+        if isinstance(x, QuantizedActivation):
+            # codes + scales from a producer kernel with the quantization fused in
+            return apply_w8a8_linear(x.xq, x.scales, layer.qweight, layer.w_scales, bias=bias, out_dtype=x.dtype,
+                                     out_shape=(*x.shape[:-1], layer.qweight.shape[0]))
         if _native(x, layer.qweight, layer.w_scales, bias):
             # quantize + GEMM in one ABI call (reference w8a8.py:25-40 does
             # quantize_activation then apply_w8a8_linear; same numerics).
