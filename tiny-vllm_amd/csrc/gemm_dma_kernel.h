@@ -30,6 +30,17 @@
 // Waits are explicit: the compiler does not track LDS-DMA completion, so each
 // step waits on vmcnt for its own stage and then crosses an s_barrier (a bare
 // barrier, without the workgroup fence that would force vmcnt(0)).
+//
+// The grid is persistent when there are more tiles than resident workgroups:
+// each workgroup walks tiles blockIdx.x, +gridDim.x, ... After the last
+// k-stage of a tile it issues the first S-1 stages of its next tile into ring
+// slots 0..S-2 and only then runs the epilogue, so the operand fetch of tile
+// i+1 overlaps the output stores of tile i. The epilogue needs no global
+// loads (which would queue behind that DMA): the tile's per-token scales,
+// per-channel scales and bias are fetched at tile start and parked in LDS.
+// It stages each wave's MF-row slice of its output through a wave-private
+// area of the idle ring slot S-1 and writes whole row segments of 16-byte
+// stores.
 #pragma once
 
 #include <type_traits>
@@ -75,16 +86,20 @@ struct Cfg {
   static constexpr int kXBlk = (BM / 8) * kXHalves;       // activation blocks per stage
   static constexpr int kBlkStage = kWBlk + kXBlk;
   static constexpr int kStageBytes = kBlkStage * 1024;
-  static constexpr int kLdsBytes = kStageBytes * S;
+  static constexpr int kRingBytes = kStageBytes * S;
   static constexpr int kLPW = kBlkStage / kWaves;         // DMA ops per wave per stage
   static constexpr int kKStage = 128;                     // k values per stage
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / MF, FN = TN / MF;        // MFMA tiles per wave
+  static constexpr int kEpiBytes = MF * TN * 2;           // per-wave staging: MF rows x TN 16-bit outputs
+  static constexpr int kScN = BM + 2 * BN;                // per-tile a_scales | w_scales | bias (fp32, in LDS)
+  static constexpr int kLdsBytes = kRingBytes + kScN * 4;
   static_assert(MF == 16 || MF == 32, "MFMA tile is 16x16 or 32x32");
   static_assert(kBlkStage % kWaves == 0, "stage blocks must split evenly over waves");
   static_assert(TM % MF == 0 && TN % MF == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(S >= 2, "at least double buffering");
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+  static_assert(kWaves * kEpiBytes <= kStageBytes, "epilogue staging must fit in one ring stage");
 };
 
 // Store four consecutive outputs y[m, nb..nb+3] with the path's epilogue.
@@ -134,33 +149,13 @@ __device__ __forceinline__ int chunk_off(int row, int c) {
   return (row >> 3) * 1024 + 16 * (rho * 8 + (c ^ rho));
 }
 
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
-                                                                const float* __restrict__ a_scales,
-                                                                const int8_t* __restrict__ qw,
-                                                                const float* __restrict__ ws,
-                                                                const uint16_t* __restrict__ bias,
-                                                                void* __restrict__ yv, int M, int N, int K,
-                                                                int group, int m_major) {
-  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
-  using Acc = typename std::conditional<
-      MF == 32, typename std::conditional<kW8A8, i32x16, f32x16>::type,
-      typename std::conditional<kW8A8, i32x4, f32x4>::type>::type;
-  constexpr int kAccN = MF == 32 ? 16 : 4;
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wn = wave % WN;
-  const int wm = wave / WN;
-
-  // ---- tile order: XCD chunking, then grouped swizzle -------------------
-  const int tiles_m = (M + BM - 1) / BM;
-  const int tiles_n = (N + BN - 1) / BN;
+// Tile order: XCD chunking (workgroup i runs on XCD i % 8, so each XCD gets a
+// contiguous range of logical tiles), then a grouped swizzle so that the
+// tiles in flight on one XCD share operand panels in its L2.
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int group, int m_major, int& tm,
+                                            int& tn) {
   const int total = tiles_m * tiles_n;
-  int pid = blockIdx.x;
   if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
-  int tm, tn;
   if (m_major) {
     // consecutive tiles walk m inside groups of `group` n-tiles
     const int per_group = group * tiles_m;
@@ -178,40 +173,67 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     tm = first + in % gsz;
     tn = in / gsz;
   }
-  const int n0 = tn * BN;
-  const int m0 = tm * BM;
+}
+
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
+                                                                const float* __restrict__ a_scales,
+                                                                const int8_t* __restrict__ qw,
+                                                                const float* __restrict__ ws,
+                                                                const uint16_t* __restrict__ bias,
+                                                                void* __restrict__ yv, int M, int N, int K,
+                                                                int group, int m_major) {
+  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
+  using Acc = typename std::conditional<
+      MF == 32, typename std::conditional<kW8A8, i32x16, f32x16>::type,
+      typename std::conditional<kW8A8, i32x4, f32x4>::type>::type;
+  constexpr int kAccN = MF == 32 ? 16 : 4;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar registers
+  const int wn = wave % WN;
+  const int wm = wave / WN;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int total = tiles_m * tiles_n;
+  const int nk = K / C::kKStage;
 
   // ---- per-lane DMA sources for this wave's blocks ----------------------
-  const char* src[C::kLPW];
-  int ldsoff[C::kLPW];
-  int stride[C::kLPW];
-  {
-    const int rho = lane >> 3;           // row within the 8-row block
-    const int chunk = (lane & 7) ^ rho;  // 16-byte chunk this lane fetches
+  // Each source is a wave-uniform tile base (scalar registers) plus a 32-bit
+  // per-lane offset, which keeps the address state of the kLPW streams small.
+  const char* wbase = reinterpret_cast<const char*>(qw);
+  const char* xbase = static_cast<const char*>(xv);
+  int soff[C::kLPW];
+  const int drho = lane >> 3;             // row within the 8-row block
+  const int dchunk = (lane & 7) ^ drho;   // 16-byte chunk this lane fetches
+  auto set_sources = [&](int m0, int n0) {
+    wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K;
+    xbase = static_cast<const char*>(xv) + (int64_t)m0 * K * (kW8A8 ? 1 : 2);
 #pragma unroll
     for (int j = 0; j < C::kLPW; ++j) {
       const int b = j * C::kWaves + wave;
-      ldsoff[j] = b * 1024;
       if (b < C::kWBlk) {
-        const int n = min(n0 + 8 * b + rho, N - 1);
-        src[j] = reinterpret_cast<const char*>(qw) + (int64_t)n * K + 16 * chunk;
-        stride[j] = C::kKStage;
+        const int n = min(n0 + 8 * b + drho, N - 1) - n0;
+        soff[j] = n * K + 16 * dchunk;
       } else {
         const int xb = b - C::kWBlk;
-        const int m = min(m0 + 8 * (xb / C::kXHalves) + rho, M - 1);
+        const int m = min(m0 + 8 * (xb / C::kXHalves) + drho, M - 1) - m0;
         const int half = xb % C::kXHalves;
-        src[j] = static_cast<const char*>(xv) + (int64_t)m * K * (kW8A8 ? 1 : 2) + 128 * half + 16 * chunk;
-        stride[j] = kW8A8 ? C::kKStage : 2 * C::kKStage;
+        soff[j] = m * K * (kW8A8 ? 1 : 2) + 128 * half + 16 * dchunk;
       }
     }
-  }
-
+  };
   auto issue = [&](int kt) {
     char* stage = smem + (kt % S) * C::kStageBytes;
 #pragma unroll
-    for (int j = 0; j < C::kLPW; ++j)
-      __builtin_amdgcn_global_load_lds(TVQ_GPTR(src[j] + (int64_t)kt * stride[j]), TVQ_LPTR(stage + ldsoff[j]), 16, 0,
-                                       0);
+    for (int j = 0; j < C::kLPW; ++j) {
+      const int b = j * C::kWaves + wave;
+      const bool wblk = b < C::kWBlk;
+      const int step = (wblk || kW8A8) ? C::kKStage : 2 * C::kKStage;
+      const char* p = (wblk ? wbase : xbase) + soff[j] + (int64_t)kt * step;
+      __builtin_amdgcn_global_load_lds(TVQ_GPTR(p), TVQ_LPTR(stage + b * 1024), 16, 0, 0);
+    }
   };
 
   // ---- lane-constant fragment offsets within a stage ---------------------
@@ -239,161 +261,242 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   constexpr int kWFrag = kRows / 8 * 1024;         // bytes per weight fragment (rows x 128 B)
   constexpr int kXFrag = kW8A8 ? kWFrag : 2 * kWFrag;
 
-  Acc acc[C::FN][C::FM];
+  // ---- per-tile scales and bias, parked in LDS for the epilogue ----------
+  float* sc = reinterpret_cast<float*>(smem + C::kRingBytes);  // [a_s: BM | w_s: BN | bias: BN]
+  constexpr int kScPer = (C::kScN + C::kThreads - 1) / C::kThreads;
+  float scv[kScPer];
+  auto load_scales = [&](int m0, int n0) {
 #pragma unroll
-  for (int i = 0; i < C::FN; ++i)
+    for (int u = 0; u < kScPer; ++u) {
+      const int idx = (int)threadIdx.x + u * C::kThreads;
+      float v = 0.0f;
+      if (idx < BM) {
+        if constexpr (kW8A8) v = a_scales[min(m0 + idx, M - 1)];
+      } else if (idx < BM + BN) {
+        v = ws[min(n0 + idx - BM, N - 1)];
+      } else if (idx < C::kScN && bias != nullptr) {
+        v = to_float<T>(bias[min(n0 + idx - BM - BN, N - 1)]);
+      }
+      scv[u] = v;
+    }
+  };
+  auto store_scales = [&]() {
 #pragma unroll
-    for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
+    for (int u = 0; u < kScPer; ++u) {
+      const int idx = (int)threadIdx.x + u * C::kThreads;
+      if (idx < C::kScN) sc[idx] = scv[u];
+    }
+  };
 
-  const int nk = K / C::kKStage;
+  int tile = blockIdx.x;
+  int tm, tn;
+  tile_coords(tile, tiles_m, tiles_n, group, m_major, tm, tn);
+  set_sources(tm * BM, tn * BN);
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
     if (s < nk) issue(s);
+  if constexpr (!kRaw) load_scales(tm * BM, tn * BN);
 
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_stage<C::kLPW, S>(min(S - 2, nk - 1 - kt));
-    barrier();
-    if (kt + S - 1 < nk) issue(kt + S - 1);
+  while (true) {
+    const int n0 = tn * BN;
+    const int m0 = tm * BM;
+    Acc acc[C::FN][C::FM];
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
 
-    const char* wst = smem + (kt % S) * C::kStageBytes + wn * C::FN * kWFrag;
-    const char* xst = smem + (kt % S) * C::kStageBytes + C::kWBlk * 1024 + wm * C::FM * kXFrag;
-    // Fragments are double-buffered in registers: the LDS reads of sub-step
-    // ks+1 are issued before the MFMAs of sub-step ks, so their latency hides
-    // behind the matrix core instead of stalling the wave.
-    u32x4 fa[2][C::FN];
-    u32x4 fb[2][C::FM][kW8A8 ? 1 : 2];
-    auto load_frags = [&](int ks, int buf) {
-#pragma unroll
-      for (int i = 0; i < C::FN; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(wst + i * kWFrag + woff[ks]);
-#pragma unroll
-      for (int j = 0; j < C::FM; ++j) {
-        if constexpr (kW8A8) {
-          fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + woff[ks]);
-        } else {
-          fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][0]);
-          fb[buf][j][1] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][1]);
-        }
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_stage<C::kLPW, S>(min(S - 2, nk - 1 - kt));
+      barrier();
+      if constexpr (!kRaw) {
+        // after the barrier: the previous tile's epilogue no longer reads them
+        if (kt == 0) store_scales();
       }
-    };
-    load_frags(0, 0);
+      if (kt + S - 1 < nk) issue(kt + S - 1);
+
+      const char* wst = smem + (kt % S) * C::kStageBytes + wn * C::FN * kWFrag;
+      const char* xst = smem + (kt % S) * C::kStageBytes + C::kWBlk * 1024 + wm * C::FM * kXFrag;
+      // Fragments are double-buffered in registers: the LDS reads of sub-step
+      // ks+1 are issued before the MFMAs of sub-step ks, so their latency hides
+      // behind the matrix core instead of stalling the wave.
+      u32x4 fa[2][C::FN];
+      u32x4 fb[2][C::FM][kW8A8 ? 1 : 2];
+      auto load_frags = [&](int ks, int buf) {
 #pragma unroll
-    for (int ks = 0; ks < kSub; ++ks) {
-      const int cb = ks & 1;
-      if (ks + 1 < kSub) load_frags(ks + 1, cb ^ 1);
-      // Keep the scheduler from sinking those reads below this sub-step's MFMAs.
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (kW8A8) {
+        for (int i = 0; i < C::FN; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(wst + i * kWFrag + woff[ks]);
 #pragma unroll
         for (int j = 0; j < C::FM; ++j) {
-#pragma unroll
-          for (int i = 0; i < C::FN; ++i) {
-            if constexpr (MF == 32)
-              acc[i][j] = mfma32x32x32_i8(fa[cb][i], fb[cb][j][0], acc[i][j]);
-            else
-              acc[i][j] = mfma16x16x64_i8(fa[cb][i], fb[cb][j][0], acc[i][j]);
+          if constexpr (kW8A8) {
+            fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + woff[ks]);
+          } else {
+            fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][0]);
+            fb[buf][j][1] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][1]);
           }
         }
-      } else {
+      };
+      load_frags(0, 0);
 #pragma unroll
-        for (int i = 0; i < C::FN; ++i) {
-          const u32x2 c0 = i8x4_to_16x4<T>(fa[cb][i][0]);
-          const u32x2 c1 = i8x4_to_16x4<T>(fa[cb][i][1]);
-          const u32x2 c2 = i8x4_to_16x4<T>(fa[cb][i][2]);
-          const u32x2 c3 = i8x4_to_16x4<T>(fa[cb][i][3]);
-          const u32x4 alo = u32x4{c0.x, c0.y, c1.x, c1.y};
-          const u32x4 ahi = u32x4{c2.x, c2.y, c3.x, c3.y};
+      for (int ks = 0; ks < kSub; ++ks) {
+        const int cb = ks & 1;
+        if (ks + 1 < kSub) load_frags(ks + 1, cb ^ 1);
+        // Keep the scheduler from sinking those reads below this sub-step's MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kW8A8) {
 #pragma unroll
           for (int j = 0; j < C::FM; ++j) {
-            if constexpr (MF == 32) {
-              acc[i][j] = mfma32x32x16<T>(alo, fb[cb][j][0], acc[i][j]);
-              acc[i][j] = mfma32x32x16<T>(ahi, fb[cb][j][1], acc[i][j]);
-            } else {
-              acc[i][j] = mfma16x16x32<T>(alo, fb[cb][j][0], acc[i][j]);
-              acc[i][j] = mfma16x16x32<T>(ahi, fb[cb][j][1], acc[i][j]);
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i) {
+              if constexpr (MF == 32)
+                acc[i][j] = mfma32x32x32_i8(fa[cb][i], fb[cb][j][0], acc[i][j]);
+              else
+                acc[i][j] = mfma16x16x64_i8(fa[cb][i], fb[cb][j][0], acc[i][j]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < C::FN; ++i) {
+            const u32x2 c0 = i8x4_to_16x4<T>(fa[cb][i][0]);
+            const u32x2 c1 = i8x4_to_16x4<T>(fa[cb][i][1]);
+            const u32x2 c2 = i8x4_to_16x4<T>(fa[cb][i][2]);
+            const u32x2 c3 = i8x4_to_16x4<T>(fa[cb][i][3]);
+            const u32x4 alo = u32x4{c0.x, c0.y, c1.x, c1.y};
+            const u32x4 ahi = u32x4{c2.x, c2.y, c3.x, c3.y};
+#pragma unroll
+            for (int j = 0; j < C::FM; ++j) {
+              if constexpr (MF == 32) {
+                acc[i][j] = mfma32x32x16<T>(alo, fb[cb][j][0], acc[i][j]);
+                acc[i][j] = mfma32x32x16<T>(ahi, fb[cb][j][1], acc[i][j]);
+              } else {
+                acc[i][j] = mfma16x16x32<T>(alo, fb[cb][j][0], acc[i][j]);
+                acc[i][j] = mfma16x16x32<T>(ahi, fb[cb][j][1], acc[i][j]);
+              }
             }
           }
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
-  }
 
-  // ---- epilogue -----------------------------------------------------------
-  // MF 16: acc reg t -> n = 4g + t.  MF 32: reg v -> n = 8*(v/4) + 4g + v%4.
-  // Either way a lane owns runs of 4 consecutive output channels of token r.
-  if constexpr (kRaw) {
+    // Every wave has consumed its last fragments: the ring is free.
+    barrier();
+    // ---- next tile: start its operand stream before this tile's stores ----
+    const int next = tile + (int)gridDim.x;
+    const bool more = next < total;
+    if (more) {
+      tile = next;
+      tile_coords(tile, tiles_m, tiles_n, group, m_major, tm, tn);
+      set_sources(tm * BM, tn * BN);
 #pragma unroll
-    for (int j = 0; j < C::FM; ++j) {
-      const int m = m0 + wm * C::TM + MF * j + r;
-      if (m >= M) continue;
-#pragma unroll
-      for (int i = 0; i < C::FN; ++i) {
-        const Acc v = acc[i][j];
-#pragma unroll
-        for (int q = 0; q < kAccN / 4; ++q) {
-          const int nb = n0 + wn * C::TN + MF * i + 8 * q + 4 * g;
-          store4<T, kW8A8, kRaw>(yv, ws, bias, 0.0f, m, nb, N, v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-        }
-      }
+      for (int s = 0; s < S - 1; ++s)
+        if (s < nk) issue(s);
+      if constexpr (!kRaw) load_scales(tm * BM, tn * BN);
     }
-  } else {
-    // Stage the finished 16-bit tile in LDS (the operand ring is free now),
-    // then write whole rows with coalesced 16-byte stores. Row m of the tile
-    // is 2*BN bytes; its 16-byte chunks are XOR-swizzled by (m & 15) so the
-    // 4-element writes of 16+ different rows land on different banks.
-    static_assert(BM * BN * 2 <= C::kLdsBytes, "output tile must fit in the LDS ring");
-    constexpr int kChunks = BN / 8;
-    constexpr int kSwz = (kChunks < 16 ? kChunks : 16) - 1;
-    __syncthreads();
-    auto toff = [&](int ml, int nl) { return ml * (2 * BN) + 16 * ((nl >> 3) ^ (ml & kSwz)) + 2 * (nl & 7); };
+
+    // ---- epilogue -----------------------------------------------------------
+    // MF 16: acc reg t -> n = 4g + t.  MF 32: reg v -> n = 8*(v/4) + 4g + v%4.
+    // Either way a lane owns runs of 4 consecutive output channels of token r.
+    constexpr int kQ = kAccN / 4;
+    const int ncol0 = n0 + wn * C::TN;             // first output column of the wave tile
+    if constexpr (kRaw) {
 #pragma unroll
-    for (int j = 0; j < C::FM; ++j) {
-      const int ml = wm * C::TM + MF * j + r;
-      const int m = min(m0 + ml, M - 1);
-      float as = 0.0f;
-      if constexpr (kW8A8) as = a_scales[m];
+      for (int j = 0; j < C::FM; ++j) {
+        const int m = m0 + wm * C::TM + MF * j + r;
+        if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < C::FN; ++i) {
-        const Acc v = acc[i][j];
+        for (int i = 0; i < C::FN; ++i) {
+          const Acc v = acc[i][j];
 #pragma unroll
-        for (int q = 0; q < kAccN / 4; ++q) {
-          const int nl = wn * C::TN + MF * i + 8 * q + 4 * g;
-          float o[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int n = min(n0 + nl + t, N - 1);
-            const float bb = bias ? to_float<T>(bias[n]) : 0.0f;
-            if constexpr (kW8A8)
-              o[t] = epi_w8a8(v[4 * q + t], as, ws[n], bb);
-            else
-              o[t] = epi_w8a16(v[4 * q + t], ws[n], bb);
+          for (int q = 0; q < kQ; ++q) {
+            const int nb = ncol0 + MF * i + 8 * q + 4 * g;
+            store4<T, kW8A8, kRaw>(yv, ws, bias, 0.0f, m, nb, N, v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
           }
-          u32x2 pk;
-          pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
-          pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
-          *reinterpret_cast<u32x2*>(smem + toff(ml, nl)) = pk;
         }
       }
-    }
-    __syncthreads();
-    const bool vec = (N & 7) == 0;
-    uint16_t* y = static_cast<uint16_t*>(yv);
-    for (int c = threadIdx.x; c < BM * kChunks; c += C::kThreads) {
-      const int ml = c / kChunks;
-      const int cl = c % kChunks;
-      const int m = m0 + ml;
-      const int n = n0 + 8 * cl;
-      if (m >= M || n >= N) continue;
-      const u32x4 val = *reinterpret_cast<const u32x4*>(smem + ml * (2 * BN) + 16 * (cl ^ (ml & kSwz)));
-      uint16_t* dst = y + (int64_t)m * N + n;
-      if (vec && n + 8 <= N) {
-        *reinterpret_cast<u32x4*>(dst) = val;
-      } else {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(&val);
-        for (int t = 0; t < 8 && n + t < N; ++t) dst[t] = h[t];
+    } else {
+      // Per MF-row slice of the wave tile: scale and round, write to the
+      // wave's staging area (row stride 2*TN bytes; 16-byte chunk index XORed
+      // with the row so the column-aligned writes of different rows use
+      // different banks), then read it back row-contiguous and store 16 bytes
+      // per lane: every row segment of the slice leaves as whole 2*TN-byte runs.
+      constexpr int kRowB = 2 * C::TN;             // bytes per staged row
+      constexpr int kCh = kRowB / 16;              // 16-byte chunks per row
+      constexpr int kSwz = (kCh < 8 ? kCh : 8) - 1;
+      constexpr int kPass = MF * kCh / 64;         // read-back passes per slice
+      static_assert((MF * kCh) % 64 == 0, "slice must split evenly over the wave");
+      char* stg = smem + (S - 1) * C::kStageBytes + wave * C::kEpiBytes;
+      const float* sc_w = sc + BM + wn * C::TN;
+      const float* sc_b = sc + BM + BN + wn * C::TN;
+      uint16_t* y = static_cast<uint16_t*>(yv);
+      const bool vec = (N & 7) == 0;
+#pragma unroll
+      for (int j = 0; j < C::FM; ++j) {
+        const int mrow0 = m0 + wm * C::TM + MF * j;  // first output row of this slice
+        float as = 0.0f;
+        if constexpr (kW8A8) as = sc[wm * C::TM + MF * j + r];
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) {
+#pragma unroll
+          for (int q = 0; q < kQ; ++q) {
+            const int nl = MF * i + 8 * q + 4 * g;   // column within the wave tile (multiple of 4)
+            const f32x4 wv = *reinterpret_cast<const f32x4*>(sc_w + nl);
+            const f32x4 bv = *reinterpret_cast<const f32x4*>(sc_b + nl);
+            float o[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              if constexpr (kW8A8)
+                o[t] = epi_w8a8(acc[i][j][4 * q + t], as, wv[t], bv[t]);
+              else
+                o[t] = epi_w8a16(acc[i][j][4 * q + t], wv[t], bv[t]);
+            }
+            u32x2 pk;
+            pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
+            pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
+            *reinterpret_cast<u32x2*>(stg + r * kRowB + 16 * ((nl >> 3) ^ (r & kSwz)) + 2 * (nl & 7)) = pk;
+          }
+        }
+        // LDS operations of one wave complete in order; the wait and the
+        // compiler barrier keep the read-back after the writes above.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int ps = 0; ps < kPass; ++ps) {
+          const int e = ps * 64 + lane;
+          const int row = e / kCh;
+          const int ch = e % kCh;
+          const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kRowB + 16 * (ch ^ (row & kSwz)));
+          const int mo = mrow0 + row;
+          const int no = ncol0 + 8 * ch;
+          if (mo < M && no < N) {
+            uint16_t* dst = y + (int64_t)mo * N + no;
+            if (vec && no + 8 <= N) {
+              *reinterpret_cast<u32x4*>(dst) = val;
+            } else {
+#pragma unroll
+              for (int t = 0; t < 8; ++t)
+                if (no + t < N) dst[t] = (uint16_t)(val[t >> 1] >> (16 * (t & 1)));
+            }
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
     }
+    if (!more) break;
   }
+}
+
+// Workgroups one CU holds for a given LDS footprint, times the CU count of the
+// current device (cached per device): the persistent grid size.
+inline int resident_workgroups(int lds_bytes) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cus[dev] = n;
+  }
+  const int per_cu = lds_bytes > 0 ? (160 * 1024) / lds_bytes : 1;
+  return cus[dev] * (per_cu > 0 ? per_cu : 1);
 }
 
 // Host-side launcher for one configuration.
@@ -410,8 +513,11 @@ hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const f
     attr_set = true;
   }
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  kern<<<dim3(tiles), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias),
-                                                                  y, M, N, K, group, m_major);
+  int grid = tiles;
+  const int resident = resident_workgroups(C::kLdsBytes);
+  if (resident > 0 && tiles > resident) grid = resident - resident % 8;  // keep whole XCD rounds
+  kern<<<dim3(grid), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias),
+                                                                 y, M, N, K, group, m_major);
   return hipGetLastError();
 }
 
