@@ -5,11 +5,15 @@
 // S-1 stages of loads are in flight while the MFMAs of the current one run.
 //
 // One wave-level DMA fills one 1 KB block: 8 rows x 128 contiguous bytes of
-// the operand (full cache lines). Lane i fetches row i/8, 16-byte chunk
-// c = (i%8) ^ (i/8) of that row, and the hardware writes it to block + 16*i;
-// so chunk c of row rho sits in slot rho*8 + (c ^ rho). The XOR spreads the
-// 16 rows a fragment read touches across all LDS banks (no conflicts) while
-// every DMA still reads whole 128-byte lines.
+// the operand (full cache lines). Lane i fetches row rho = i/8 of the block,
+// 16-byte chunk c = (i%8) ^ swz(row), and the hardware writes it to
+// block + 16*i; so chunk c of row rho sits in slot rho*8 + (c ^ swz(row)),
+// with swz(row) = (row/2) % 8 over the row's index in the tile. The LDS
+// serves a 128-bit read 16 lanes at a time over 256 bytes of banks: rows
+// of equal parity land 256 bytes apart, and swz gives the 8 rows of each
+// parity in a 16-row group 8 different chunk slots, so the 16 lanes of a
+// fragment read (16 rows, one logical chunk) never share a bank, while every
+// DMA still reads whole 128-byte lines.
 //
 // Fragment reads (one ds_read_b128 per lane, lane = 16*g + r):
 //   weight / int8 activation, 64-k sub-step ks: row r, chunk 4*ks + g
@@ -143,10 +147,11 @@ __device__ __forceinline__ void store4(void* yv, const float* ws, const uint16_t
 }
 
 // Offset (bytes) of 16-byte chunk `c` of row `row` inside a run of 8-row
-// blocks laid out by the DMA (chunk c of row rho at slot rho*8 + (c ^ rho)).
+// blocks laid out by the DMA (chunk c of row rho at slot rho*8 + (c ^ swz)).
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
 __device__ __forceinline__ int chunk_off(int row, int c) {
-  const int rho = row & 7;
-  return (row >> 3) * 1024 + 16 * (rho * 8 + (c ^ rho));
+  return (row >> 3) * 1024 + 16 * ((row & 7) * 8 + (c ^ swz(row)));
 }
 
 // Tile order: XCD chunking (workgroup i runs on XCD i % 8, so each XCD gets a
@@ -206,7 +211,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   const char* xbase = static_cast<const char*>(xv);
   int soff[C::kLPW];
   const int drho = lane >> 3;             // row within the 8-row block
-  const int dchunk = (lane & 7) ^ drho;   // 16-byte chunk this lane fetches
   auto set_sources = [&](int m0, int n0) {
     wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K;
     xbase = static_cast<const char*>(xv) + (int64_t)m0 * K * (kW8A8 ? 1 : 2);
@@ -214,13 +218,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     for (int j = 0; j < C::kLPW; ++j) {
       const int b = j * C::kWaves + wave;
       if (b < C::kWBlk) {
-        const int n = min(n0 + 8 * b + drho, N - 1) - n0;
-        soff[j] = n * K + 16 * dchunk;
+        const int row = 8 * b + drho;                       // row of the tile's weight panel
+        const int n = min(n0 + row, N - 1) - n0;
+        soff[j] = n * K + 16 * ((lane & 7) ^ swz(row));
       } else {
         const int xb = b - C::kWBlk;
-        const int m = min(m0 + 8 * (xb / C::kXHalves) + drho, M - 1) - m0;
+        const int row = 8 * (xb / C::kXHalves) + drho;      // row of the tile's activation panel
+        const int m = min(m0 + row, M - 1) - m0;
         const int half = xb % C::kXHalves;
-        soff[j] = m * K * (kW8A8 ? 1 : 2) + 128 * half + 16 * dchunk;
+        soff[j] = m * K * (kW8A8 ? 1 : 2) + 128 * half + 16 * ((lane & 7) ^ swz(row));
       }
     }
   };
@@ -255,7 +261,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       // 16-bit activations: k = ks*(128/kSub) + 16*g + 8*b .. +8, two 64-k halves per row
       const int k = ks * (128 / kSub) + 16 * g + 8 * b;
       const int rho = r & 7;
-      xoff[ks][b] = (r >> 3) * 2048 + (k >> 6) * 1024 + 16 * (rho * 8 + (((k & 63) >> 3) ^ rho));
+      xoff[ks][b] = (r >> 3) * 2048 + (k >> 6) * 1024 + 16 * (rho * 8 + (((k & 63) >> 3) ^ swz(r)));
     }
   }
   constexpr int kWFrag = kRows / 8 * 1024;         // bytes per weight fragment (rows x 128 B)
@@ -416,12 +422,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     } else {
       // Per MF-row slice of the wave tile: scale and round, write to the
       // wave's staging area (row stride 2*TN bytes; 16-byte chunk index XORed
-      // with the row so the column-aligned writes of different rows use
-      // different banks), then read it back row-contiguous and store 16 bytes
-      // per lane: every row segment of the slice leaves as whole 2*TN-byte runs.
+      // with (row / rows-per-256-bytes) so the column-aligned writes of 16
+      // consecutive rows use different banks), then read it back
+      // row-contiguous and store 16 bytes per lane: every row segment of the
+      // slice leaves as whole 2*TN-byte runs.
       constexpr int kRowB = 2 * C::TN;             // bytes per staged row
       constexpr int kCh = kRowB / 16;              // 16-byte chunks per row
       constexpr int kSwz = (kCh < 8 ? kCh : 8) - 1;
+      constexpr int kRowsPer256 = kRowB >= 256 ? 1 : 256 / kRowB;
+      auto sswz = [](int row) { return (row / kRowsPer256) & kSwz; };
       constexpr int kPass = MF * kCh / 64;         // read-back passes per slice
       static_assert((MF * kCh) % 64 == 0, "slice must split evenly over the wave");
       char* stg = smem + (S - 1) * C::kStageBytes + wave * C::kEpiBytes;
@@ -452,7 +461,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
             u32x2 pk;
             pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
             pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
-            *reinterpret_cast<u32x2*>(stg + r * kRowB + 16 * ((nl >> 3) ^ (r & kSwz)) + 2 * (nl & 7)) = pk;
+            *reinterpret_cast<u32x2*>(stg + r * kRowB + 16 * ((nl >> 3) ^ sswz(r)) + 2 * (nl & 7)) = pk;
           }
         }
         // LDS operations of one wave complete in order; the wait and the
@@ -463,7 +472,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
           const int e = ps * 64 + lane;
           const int row = e / kCh;
           const int ch = e % kCh;
-          const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kRowB + 16 * (ch ^ (row & kSwz)));
+          const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kRowB + 16 * (ch ^ sswz(row)));
           const int mo = mrow0 + row;
           const int no = ncol0 + 8 * ch;
           if (mo < M && no < N) {
