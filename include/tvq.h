@@ -141,6 +141,30 @@ int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps,
 int tvq_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales,
                  int dtype, int64_t M, int64_t I, void* stream);
 
+/* Decode attention with the KV-cache append, one query token per sequence.
+ * Replaces the decode branch of Attention.forward
+ * (nanovllm/layers/attention.py:59-88: store_kvcache then
+ * flash_attn_with_kvcache(..., cache_seqlens, causal=True)).
+ *   q      [B, Hq, head_dim]   row stride q_stride (elements) between tokens
+ *   k_new, v_new [B, Hkv, head_dim]  row strides k_stride / v_stride
+ *   k_cache, v_cache [num_slots, Hkv, max_len, head_dim] (a slot per sequence)
+ *   slots, lens [B] int32: sequence b owns slot slots[b] and has lens[b]
+ *          tokens including the new one (1 <= lens[b] <= max_len); a
+ *          sequence whose slot or length is out of range gets zeros and its
+ *          cache is not touched
+ *   out    [B, Hq, head_dim] contiguous
+ * Writes k_new/v_new at position lens[b]-1 of the slot, then
+ * out = softmax(scale * q K^T) V over positions 0..lens[b]-1 (fp32 math).
+ * head_dim must be 128, Hq/Hkv in {1, 2, 4}, all pointers 16-byte aligned and
+ * strides multiples of 8. Lengths and slots are read on the device: safe in
+ * HIP-graph capture. */
+int tvq_decode_attention(const void* q, int64_t q_stride, const void* k_new,
+                         int64_t k_stride, const void* v_new, int64_t v_stride,
+                         void* k_cache, void* v_cache, const int32_t* slots,
+                         const int32_t* lens, int64_t B, int Hq, int Hkv,
+                         int head_dim, int64_t num_slots, int64_t max_len,
+                         float scale, void* out, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,102 @@
+"""GPU tests of the decode-attention kernel (tvq_decode_attention) against a
+plain PyTorch fp32 reference of the reference's decode step
+(attention.py:59-88: store_kvcache, then flash_attn_with_kvcache with
+cache_seqlens, causal): the appended K/V row is bit-exact, every other cache
+entry is untouched, and the output is within bf16 rounding of the fp32
+reference (max-abs <= 1e-2 * max|ref| + 1e-3)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(q, kc, vc, slots, lens, scale):
+    out = []
+    hq, hkv = q.shape[1], kc.shape[1]
+    for b in range(q.shape[0]):
+        n = int(lens[b])
+        k = kc[int(slots[b]), :, :n].float().repeat_interleave(hq // hkv, 0)  # [Hq, n, D]
+        v = vc[int(slots[b]), :, :n].float().repeat_interleave(hq // hkv, 0)
+        p = torch.softmax((q[b].float()[:, None, :] @ k.transpose(1, 2)).squeeze(1) * scale, -1)  # [Hq, n]
+        out.append((p[:, None, :] @ v).squeeze(1))
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_attention_matches_fp32_reference(hiplib, hq, hkv, dtype):
+    from nanovllm.quantization import _hip
+    print(f"CASE decode_attention hq={hq} hkv={hkv} dtype={dtype}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(hq * 10 + hkv)
+    n_slots, max_len, d = 12, 1100, 128
+    kc = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).to(dtype)
+    vc = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).to(dtype)
+    lens_l = [1, 2, 17, 16, 33, 100, 1000, 1100, 257]
+    slots_l = [3, 0, 11, 5, 7, 1, 2, 9, 10]
+    b = len(lens_l)
+    # q / k / v as strided views of a packed qkv row, as the model produces them
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, device="cuda", generator=g).to(dtype)
+    q = qkv[:, : hq * d].view(b, hq, d)
+    k = qkv[:, hq * d: (hq + hkv) * d].view(b, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+    slots = torch.tensor(slots_l, dtype=torch.int32, device="cuda")
+    lens = torch.tensor(lens_l, dtype=torch.int32, device="cuda")
+    kc0, vc0 = kc.clone(), vc.clone()
+    scale = d ** -0.5
+    out = _hip.decode_attention(q, k, v, kc, vc, slots, lens, scale)
+    torch.cuda.synchronize()
+    # cache: new rows appended, everything else unchanged
+    exp_k, exp_v = kc0.clone(), vc0.clone()
+    for i in range(b):
+        exp_k[slots_l[i], :, lens_l[i] - 1] = k[i]
+        exp_v[slots_l[i], :, lens_l[i] - 1] = v[i]
+    assert torch.equal(kc, exp_k) and torch.equal(vc, exp_v)
+    ref = _ref(q, exp_k, exp_v, slots, lens, scale)
+    err = (out.float() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item() + 1e-3, err
+
+
+def test_decode_attention_invalid_metadata_is_inert(hiplib):
+    from nanovllm.quantization import _hip
+    kc = torch.randn(2, 8, 64, 128, device="cuda").bfloat16()
+    vc = torch.randn(2, 8, 64, 128, device="cuda").bfloat16()
+    kc0, vc0 = kc.clone(), vc.clone()
+    q = torch.randn(3, 16, 128, device="cuda").bfloat16()
+    k = torch.randn(3, 8, 128, device="cuda").bfloat16()
+    slots = torch.tensor([0, 5, 1], dtype=torch.int32, device="cuda")   # slot 5 out of range
+    lens = torch.tensor([65, 3, 0], dtype=torch.int32, device="cuda")   # 65 > max_len, 0 < 1
+    out = _hip.decode_attention(q, k, k, kc, vc, slots, lens, 0.1)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
+    assert torch.count_nonzero(out) == 0
+
+
+def test_decode_attention_in_graph_replays(hiplib):
+    """Captured once, replayed with new lengths written into the same buffers."""
+    from nanovllm.quantization import _hip
+    kc = torch.randn(4, 8, 256, 128, device="cuda").bfloat16()
+    vc = torch.randn(4, 8, 256, 128, device="cuda").bfloat16()
+    q = torch.randn(4, 16, 128, device="cuda").bfloat16()
+    k = torch.randn(4, 8, 128, device="cuda").bfloat16()
+    v = torch.randn(4, 8, 128, device="cuda").bfloat16()
+    slots = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([5, 6, 7, 8], dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _hip.decode_attention(q, k, v, kc, vc, slots, lens, 0.088, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _hip.decode_attention(q, k, v, kc, vc, slots, lens, 0.088, out=out)
+    for step in range(3):
+        lens.copy_(torch.tensor([9 + step, 100 + step, 33, 200 + step], dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = _hip.decode_attention(q, k, v, kc.clone(), vc.clone(), slots, lens, 0.088)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)

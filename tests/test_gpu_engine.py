@@ -26,7 +26,7 @@ from nanovllm.utils.context import set_context
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(vocab_size=1024, hidden_size=256, intermediate_size=768, num_hidden_layers=3, num_attention_heads=4,
-             num_key_value_heads=2, head_dim=64, max_position_embeddings=512)
+             num_key_value_heads=2, head_dim=128, max_position_embeddings=512)
 
 
 def _engine(quantization, device="cuda", std=0.08):

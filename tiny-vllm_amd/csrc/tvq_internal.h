@@ -31,6 +31,10 @@ struct GemmArgs {
 bool act_quant_vec_ok(const void* x, const void* xq, int64_t K);
 hipError_t launch_rmsnorm(const void* x, void* residual, const void* weight, float eps, void* y, int8_t* xq,
                           float* a_scales, bool bf16, int64_t M, int64_t K, hipStream_t stream);
+hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* k_new, int64_t k_stride,
+                                   const void* v_new, int64_t v_stride, void* k_cache, void* v_cache,
+                                   const int32_t* slots, const int32_t* lens, int B, int Hq, int Hkv, int max_len,
+                                   int num_slots, float scale, void* out, bool bf16, hipStream_t stream);
 hipError_t launch_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales, bool bf16, int64_t M,
                            int64_t I, hipStream_t stream);
 hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,

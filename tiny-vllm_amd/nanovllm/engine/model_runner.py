@@ -131,8 +131,8 @@ class ModelRunner:
         else:
             slots = [s.slot for s in seqs]
             lens = [len(s) for s in seqs]
-            set_context(False, max_seqlen_k=max(lens), slot_mapping=self._to_gpu(slots, torch.int64),
-                        context_lens=self._to_gpu(lens, torch.int64), kv_lo=min(slots), kv_hi=max(slots) + 1)
+            set_context(False, max_seqlen_k=max(lens), slot_mapping=self._to_gpu(slots, torch.int32),
+                        context_lens=self._to_gpu(lens, torch.int32), kv_lo=min(slots), kv_hi=max(slots) + 1)
             hidden = self.model(self._to_gpu([s.last_token for s in seqs], torch.int64),
                                 self._to_gpu([n - 1 for n in lens], torch.int64))
         logits = self.model.compute_logits(hidden)

@@ -28,6 +28,7 @@ from torch import nn
 from nanovllm.layers.activation import SiluAndMul
 from nanovllm.layers.layernorm import RMSNorm
 from nanovllm.layers.linear import MergedColumnParallelLinear, QKVParallelLinear, RowParallelLinear
+from nanovllm.quantization import _hip
 from nanovllm.utils.context import get_context
 
 
@@ -99,12 +100,18 @@ class Attention(nn.Module):
                                                    vv.unsqueeze(0), is_causal=True, scale=self.scale)
                 out[a:b] = o.squeeze(0).transpose(0, 1)
             return out
-        # Decode: one new token per running sequence. The running batch owns
-        # cache slots inside [kv_lo, kv_hi); attention runs over that slice of
-        # the cache up to the longest context, as two batched matmuls on
-        # views of the cache (no copy), with a per-slot length mask. Idle
-        # slots inside the range see one position and their rows are dropped.
+        # Decode: one new token per running sequence.
         slots, lens = ctx.slot_mapping, ctx.context_lens
+        if q.is_cuda:
+            # HIP kernel: appends k/v at position lens-1 of each slot and
+            # attends over the valid prefix only; lengths are read on the
+            # device (graph-capturable).
+            return _hip.decode_attention(q, k, v, self.k_cache, self.v_cache, slots, lens, self.scale)
+        # Host path (CPU tests): the running batch owns cache slots inside
+        # [kv_lo, kv_hi); attention runs over that slice of the cache up to the
+        # longest context, with a per-slot length mask. Idle slots inside the
+        # range see one position and their rows are dropped.
+        slots, lens = slots.long(), lens.long()
         self.k_cache[slots, :, lens - 1] = k
         self.v_cache[slots, :, lens - 1] = v
         lo, hi, lmax = ctx.kv_lo, ctx.kv_hi, int(ctx.max_seqlen_k)

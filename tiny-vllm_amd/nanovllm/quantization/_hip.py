@@ -43,6 +43,8 @@ SYMBOLS = (
     ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP)),
     ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
+    ("tvq_decode_attention", _INT, (_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _INT, _INT, _INT, _I64,
+                                    _I64, ctypes.c_float, _VP, _INT, _VP)),
 )
 
 
@@ -295,3 +297,36 @@ def silu_mul(gate_up: torch.Tensor, out: bool = True, quant: bool = False):
                               q[1].data_ptr() if q else None, _TORCH_TO_TVQ[gate_up.dtype], m, i, _stream(dev))
     _check(rc, "tvq_silu_mul")
     return y, q
+
+
+def decode_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                     v_cache: torch.Tensor, slots: torch.Tensor, lens: torch.Tensor, scale: float,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Append k_new/v_new [B, Hkv, D] at position lens-1 of each sequence's
+    cache slot and return softmax(scale q K^T) V for q [B, Hq, D]. The token
+    dimension of q / k_new / v_new may be strided (views of a packed qkv)."""
+    lib = load_library()
+    dev = q.device
+    for t in (q, k_new, v_new):
+        _require(t.is_cuda and t.dim() == 3 and t.stride(2) == 1 and t.stride(1) == t.shape[2],
+                 "q / k_new / v_new must be [B, H, D] with contiguous heads")
+    for t in (k_cache, v_cache, slots, lens):
+        _require(t.is_cuda and t.is_contiguous(), "cache / slots / lens must be contiguous GPU tensors")
+    _require(slots.dtype == torch.int32 and lens.dtype == torch.int32, "slots and lens must be int32")
+    b, hq, d = q.shape
+    hkv = k_new.shape[1]
+    _require(k_cache.dim() == 4 and k_cache.shape[1] == hkv and k_cache.shape[3] == d and
+             v_cache.shape == k_cache.shape, "caches must be [slots, Hkv, max_len, D]")
+    _require(q.dtype in _TORCH_TO_TVQ and k_cache.dtype == q.dtype, "dtype mismatch")
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=dev)
+    if b == 0:
+        return out
+    with torch.cuda.device(dev):
+        rc = lib.tvq_decode_attention(q.data_ptr(), q.stride(0), k_new.data_ptr(), k_new.stride(0), v_new.data_ptr(),
+                                      v_new.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(),
+                                      lens.data_ptr(), b, hq, hkv, d, k_cache.shape[0], k_cache.shape[2], scale,
+                                      out.data_ptr(),
+                                      _TORCH_TO_TVQ[q.dtype], _stream(dev))
+    _check(rc, "tvq_decode_attention")
+    return out
