@@ -29,9 +29,9 @@ SMALL = dict(vocab_size=1024, hidden_size=256, intermediate_size=768, num_hidden
              num_key_value_heads=2, head_dim=128, max_position_embeddings=512)
 
 
-def _engine(quantization, device="cuda", std=0.08):
+def _engine(quantization, device="cuda", std=0.08, eager=True):
     llm = LLM(Qwen3Config(**SMALL), device=device, quantization=quantization, max_model_len=256,
-              max_num_batched_tokens=512, max_num_seqs=8)
+              max_num_batched_tokens=512, max_num_seqs=8, enforce_eager=eager)
     random_init_(llm.model_runner.model, seed=3, std=std, device=device)
     return llm
 
@@ -123,7 +123,7 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
 
 
 def test_bf16_kv_cache_decode_matches_recompute(gpu):
-    llm = _engine(None)
+    llm = _engine(None, eager=False)
     prompts = [[5, 17, 33, 2, 90, 41], [100, 3], list(range(40, 160))]
     outs = llm.generate(prompts, SamplingParams(temperature=0.0, max_tokens=12, ignore_eos=True), use_tqdm=False)
     model = llm.model_runner.model
@@ -144,3 +144,19 @@ def test_quantized_engine_close_to_bf16(gpu, hiplib, mode):
     # int8 weights (and int8 activations for w8a8) perturb every projection;
     # across 3 layers the logits stay within a few percent.
     assert _rel_l2(got, ref) < (0.05 if mode == "int8" else 0.08), _rel_l2(got, ref)
+
+
+@pytest.mark.parametrize("mode", [None, "int8", "w8a8"])
+def test_decode_graph_replay_matches_eager(gpu, hiplib, mode):
+    """Decode through captured HIP graphs (batch padded to its bucket) gives
+    the same greedy tokens as eager execution, over many replays."""
+    prompts = [[5, 17, 33, 2, 90, 41], [100, 3], list(range(40, 160)), [7] * 30, [1, 2, 3]]
+    sp = SamplingParams(temperature=0.0, max_tokens=12, ignore_eos=True)
+    outs = {}
+    for eager in (True, False):
+        llm = LLM(Qwen3Config(**SMALL), quantization=mode, max_model_len=256, max_num_batched_tokens=512,
+                  max_num_seqs=8, enforce_eager=eager)
+        random_init_(llm.model_runner.model, seed=3, std=0.08)
+        assert bool(llm.model_runner.graphs) == (not eager)
+        outs[eager] = [o["token_ids"] for o in llm.generate(prompts, sp, use_tqdm=False)]
+    assert outs[True] == outs[False]

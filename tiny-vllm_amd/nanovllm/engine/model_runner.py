@@ -11,7 +11,12 @@ Owns the model, the KV cache and the sampler:
   * KV cache: one tensor [2, layers, slots, kv_heads, max_model_len, head_dim]
     whose per-layer views go to each Attention; one slot per running sequence;
   * sampling: argmax where temperature == 0, otherwise the reference's
-    exponential-race sampler (softmax(logits / T) / Exp(1), argmax).
+    exponential-race sampler (softmax(logits / T) / Exp(1), argmax);
+  * decode steps replay HIP graphs captured per batch-size bucket
+    (1, 2, 4, 8, 16, 32, ... up to min(slots, 512); reference
+    model_runner.py:214-230, 297-335) unless `enforce_eager`. The running
+    batch is padded to its bucket with slot -1 / length 0 rows, which the
+    decode-attention kernel leaves inert.
 """
 from __future__ import annotations
 
@@ -91,6 +96,9 @@ class ModelRunner:
             random_init_(self.model, config.seed, device=device)
         self.model.eval()
         self._allocate_kv_cache()
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        if device == "cuda" and not config.enforce_eager:
+            self.capture_graphs()
 
     def _allocate_kv_cache(self) -> None:
         cfg, hf = self.config, self.config.hf_config
@@ -111,6 +119,49 @@ class ModelRunner:
         for i, a in enumerate(attns):
             a.k_cache, a.v_cache = self.kv_cache[0, i], self.kv_cache[1, i]
 
+    @torch.no_grad()
+    def capture_graphs(self) -> None:
+        hf = self.config.hf_config
+        max_bs = min(self.num_slots, 512)
+        self.graph_bs = [b for b in (1, 2, 4, 8) if b <= max_bs] + list(range(16, max_bs + 1, 16))
+        if self.graph_bs[-1] < max_bs:
+            self.graph_bs.append(max_bs)
+        dev = self.device
+        gv = dict(input_ids=torch.zeros(max_bs, dtype=torch.int64, device=dev),
+                  positions=torch.zeros(max_bs, dtype=torch.int64, device=dev),
+                  slot_mapping=torch.full((max_bs,), -1, dtype=torch.int32, device=dev),
+                  context_lens=torch.zeros(max_bs, dtype=torch.int32, device=dev),
+                  outputs=torch.zeros(max_bs, hf.hidden_size, dtype=torch.bfloat16, device=dev))
+        pool = None
+        for bs in reversed(self.graph_bs):
+            graph = torch.cuda.CUDAGraph()
+            set_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs])
+            gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])  # warm-up
+            with torch.cuda.graph(graph, pool):
+                gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
+            if pool is None:
+                pool = graph.pool()
+            self.graphs[bs] = graph
+            torch.cuda.synchronize()
+            reset_context()
+        self.graph_vars = gv
+
+    def _replay_decode(self, seqs: list[Sequence]) -> torch.Tensor:
+        n = len(seqs)
+        bs = next(b for b in self.graph_bs if b >= n)
+        gv = self.graph_vars
+        pad = bs - n
+        ids = [s.last_token for s in seqs] + [0] * pad
+        pos = [len(s) - 1 for s in seqs] + [0] * pad
+        slots = [s.slot for s in seqs] + [-1] * pad
+        lens = [len(s) for s in seqs] + [0] * pad
+        gv["input_ids"][:bs].copy_(torch.tensor(ids, dtype=torch.int64, pin_memory=True), non_blocking=True)
+        gv["positions"][:bs].copy_(torch.tensor(pos, dtype=torch.int64, pin_memory=True), non_blocking=True)
+        gv["slot_mapping"][:bs].copy_(torch.tensor(slots, dtype=torch.int32, pin_memory=True), non_blocking=True)
+        gv["context_lens"][:bs].copy_(torch.tensor(lens, dtype=torch.int32, pin_memory=True), non_blocking=True)
+        self.graphs[bs].replay()
+        return gv["outputs"][:n]
+
     def _to_gpu(self, values, dtype) -> torch.Tensor:
         if self.device == "cpu":
             return torch.tensor(values, dtype=dtype)
@@ -128,6 +179,8 @@ class ModelRunner:
                         slot_mapping=torch.tensor([s.slot for s in seqs]))
             hidden = self.model(self._to_gpu(ids, torch.int64), self._to_gpu(pos, torch.int64))
             hidden = hidden[self._to_gpu(cu[1:], torch.int64) - 1]
+        elif self.graphs and len(seqs) <= self.graph_bs[-1]:
+            hidden = self._replay_decode(seqs)
         else:
             slots = [s.slot for s in seqs]
             lens = [len(s) for s in seqs]
