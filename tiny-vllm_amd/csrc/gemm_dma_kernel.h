@@ -65,20 +65,20 @@ __device__ __forceinline__ void wait_vm() {
 
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// Wait until at most `ahead` later stages (each `LPW` DMA ops) are in flight.
-template <int LPW, int S>
+// Wait until at most `ahead` later stages (each `LPW` DMA ops) are in flight
+// (0 <= ahead <= S-2); vmcnt retires in issue order.
+template <int LPW, int S, int A = S - 2>
 __device__ __forceinline__ void wait_stage(int ahead) {
   static_assert(LPW * (S - 2) < 64, "too many DMA ops in flight for vmcnt");
-  if constexpr (S >= 5) {
-    if (ahead >= 3) { wait_vm<LPW * 3>(); return; }
+  if constexpr (A <= 0) {
+    wait_vm<0>();
+  } else {
+    if (ahead >= A) {
+      wait_vm<LPW * A>();
+      return;
+    }
+    wait_stage<LPW, S, A - 1>(ahead);
   }
-  if constexpr (S >= 4) {
-    if (ahead >= 2) { wait_vm<LPW * 2>(); return; }
-  }
-  if constexpr (S >= 3) {
-    if (ahead >= 1) { wait_vm<LPW>(); return; }
-  }
-  wait_vm<0>();
 }
 
 template <bool kW8A8, int BM, int BN, int WM, int WN, int S, int MF>
