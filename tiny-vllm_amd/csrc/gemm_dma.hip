@@ -3,15 +3,18 @@
 //
 // Table (measured on MI355X over the BASELINE shapes; tile = BM x BN, waves,
 // ring depth S, MFMA shape):
-//   W8A8  many 256x256 tiles (>= 512)   256x256, 8 waves (2x4), S=2, 32x32x32 i8
+//   W8A8  >= 256 256x256 tiles          256x256, 8 waves (2x4), S=2, 32x32x32 i8
 //         >= 200 256x128 tiles          256x128, 8 waves (4x2), S=2, 32x32x32 i8
 //         M > 256                        64x64,   4 waves,       S=4, 16x16x64 i8
 //         otherwise                      32x64,   4 waves,       S=4, 16x16x64 i8
 //   W8A16 >= 200 128x256 tiles          128x256, 8 waves (2x4), S=2, 32x32x16 bf16
 //         M > 256                        64x128,  4 waves,       S=4, 32x32x16
 //         otherwise                      64x64,   4 waves,       S=4, 32x32x16
-// Large tiles amortize the L2->LDS stream (the per-CU limit of this loop);
-// small tiles keep >= 256 workgroups in flight at decode-batch M.
+// Large tiles amortize the LDS traffic, which bounds this loop: per 128-k
+// stage a 2x4-wave 256x256 tile reads 192 KB of fragments and takes 64 KB of
+// DMA writes against 2048 MFMA cycles per SIMD, i.e. ~128 B/clk, the CU's
+// LDS rate. (Fewer, larger wave tiles need 1 wave/SIMD and measured slower.)
+// Small tiles keep >= 256 workgroups in flight at decode-batch M.
 #include "gemm_dma_kernel.h"
 #include "tvq_internal.h"
 
@@ -26,7 +29,7 @@ int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm)
 
 DmaCfg choose(bool w8a8, int64_t M, int64_t N) {
   if (w8a8) {
-    if (tiles(M, N, 256, 256) >= 512) return DmaCfg::kI8_256x256;
+    if (tiles(M, N, 256, 256) >= 256) return DmaCfg::kI8_256x256;
     if (tiles(M, N, 256, 128) >= 200) return DmaCfg::kI8_256x128;
     return M > 256 ? DmaCfg::kI8_64x64 : DmaCfg::kI8_32x64;
   }

@@ -266,6 +266,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   }
   constexpr int kWFrag = kRows / 8 * 1024;         // bytes per weight fragment (rows x 128 B)
   constexpr int kXFrag = kW8A8 ? kWFrag : 2 * kWFrag;
+  constexpr int kReadsPerSub = C::FN + C::FM * (kW8A8 ? 1 : 2);   // ds_read_b128 per sub-step
+  constexpr int kMfmaPerSub = C::FN * C::FM * (kW8A8 ? 1 : 2);    // MFMAs per sub-step
 
   // ---- per-tile scales and bias, parked in LDS for the epilogue ----------
   float* sc = reinterpret_cast<float*>(smem + C::kRingBytes);  // [a_s: BM | w_s: BN | bias: BN]
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       const char* wst = smem + (kt % S) * C::kStageBytes + wn * C::FN * kWFrag;
       const char* xst = smem + (kt % S) * C::kStageBytes + C::kWBlk * 1024 + wm * C::FM * kXFrag;
       // Fragments are double-buffered in registers: the LDS reads of sub-step
-      // ks+1 are issued before the MFMAs of sub-step ks, so their latency hides
+      // ks+1 are issued among the MFMAs of sub-step ks, so their latency hides
       // behind the matrix core instead of stalling the wave.
       u32x4 fa[2][C::FN];
       u32x4 fb[2][C::FM][kW8A8 ? 1 : 2];
@@ -346,8 +348,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       for (int ks = 0; ks < kSub; ++ks) {
         const int cb = ks & 1;
         if (ks + 1 < kSub) load_frags(ks + 1, cb ^ 1);
-        // Keep the scheduler from sinking those reads below this sub-step's MFMAs.
-        __builtin_amdgcn_sched_barrier(0);
         if constexpr (kW8A8) {
 #pragma unroll
           for (int j = 0; j < C::FM; ++j) {
@@ -378,6 +378,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
                 acc[i][j] = mfma16x16x32<T>(ahi, fb[cb][j][1], acc[i][j]);
               }
             }
+          }
+        }
+        // Interleave the next sub-step's LDS reads with this sub-step's MFMAs
+        // (one read, then its share of MFMAs), so the LDS port and the matrix
+        // core work in parallel instead of in bursts.
+        if (ks + 1 < kSub) {
+#pragma unroll
+          for (int rr = 0; rr < kReadsPerSub; ++rr) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, (kMfmaPerSub + kReadsPerSub - 1) / kReadsPerSub, 0);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
