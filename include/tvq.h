@@ -165,6 +165,24 @@ int tvq_decode_attention(const void* q, int64_t q_stride, const void* k_new,
                          int head_dim, int64_t num_slots, int64_t max_len,
                          float scale, void* out, int dtype, void* stream);
 
+/* Per-head q/k RMSNorm and rotary embedding of one layer's attention input,
+ * fused. Replaces q_norm / k_norm (RMSNorm.rms_forward,
+ * nanovllm/layers/layernorm.py:16-26) followed by RotaryEmbedding.forward
+ * (nanovllm/layers/rotary_embedding.py:6-14, 36-46; rotate-half).
+ *   qkv        [T, row_stride] packed q|k|v projection output (q heads first,
+ *              then Hkv key heads; values are not read)
+ *   positions  [T] int64 (clamped to [0, max_pos))
+ *   cos_t, sin_t [max_pos, head_dim/2] fp32
+ *   q_weight, k_weight [head_dim] in `dtype`, or both NULL (rotation only)
+ *   q_out [T, Hq, head_dim], k_out [T, Hkv, head_dim] contiguous
+ * head_dim must be 128. */
+int tvq_qk_norm_rope(const void* qkv, int64_t row_stride,
+                     const int64_t* positions, const float* cos_t,
+                     const float* sin_t, const void* q_weight,
+                     const void* k_weight, float eps, int64_t T, int Hq,
+                     int Hkv, int head_dim, int64_t max_pos, void* q_out,
+                     void* k_out, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,7 +37,13 @@ def _engine(quantization, device="cuda", std=0.08, eager=True):
 
 
 def _prefill_logits(model, ids: list[int], device) -> torch.Tensor:
-    set_context(True, cu_seqlens_q=torch.tensor([0, len(ids)]), slot_mapping=None)
+    """Cache-free prefill of one sequence (no KV slot written)."""
+    n = len(ids)
+    if device == "cuda":
+        set_context(True, cu_seqlens_q=torch.tensor([0, n]), max_seqlen_q=n, num_seqs=1, slot_mapping=None,
+                    pad_index=torch.arange(n, device="cuda"))
+    else:
+        set_context(True, cu_seqlens_q=torch.tensor([0, n]), slot_mapping=None)
     with torch.no_grad():
         x = torch.tensor(ids, device=device)
         return model.compute_logits(model(x, torch.arange(len(ids), device=device))).float().cpu()

@@ -1,0 +1,97 @@
+// Per-head q/k RMSNorm + rotary embedding, fused (gfx950).
+//
+// Replaces, for the attention input of one layer, the reference's
+//   q = q_norm(q); k = k_norm(k)            (RMSNorm.rms_forward over head_dim,
+//                                            nanovllm/layers/layernorm.py:16-26)
+//   q, k = rotary_emb(positions, q, k)      (apply_rotary_emb, rotate-half,
+//                                            nanovllm/layers/rotary_embedding.py:6-14)
+// which is ~15 torch launches (casts, pow/mean/rsqrt, chunk/cat, mul/add)
+// with fp32 temporaries, by one launch that reads q and k once from the packed
+// qkv projection output and writes them once.
+//
+// One wave per (token, head), head_dim D = 128: lane i holds x[i] and
+// x[i + 64], which are exactly the pair the rotate-half rotation mixes, so
+// the rotation is lane-local; the RMS statistic is one wave reduction.
+// Rounding follows the reference step by step:
+//   n  = round(x * rsqrt(mean(x^2) + eps))     (fp32, IEEE sqrt and divide)
+//   n  = round(n * w)                           (bf16 x bf16 -> one rounding)
+//   y1 = round(n1 * cos - n2 * sin),  y2 = round(n2 * cos + n1 * sin)   (fp32)
+// With no norm weights (models with q/k bias instead of q/k norm) only the
+// rotation is applied.
+#include "tvq_common.h"
+#include "tvq_internal.h"
+
+namespace tvq {
+namespace {
+
+constexpr int kD = 128;
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <typename T, bool kNorm>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __restrict__ qkv, int64_t row_stride,
+                                                           const int64_t* __restrict__ positions,
+                                                           const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t,
+                                                           const uint16_t* __restrict__ qw,
+                                                           const uint16_t* __restrict__ kw, float eps, int T_, int Hq,
+                                                           int Hkv, int max_pos, uint16_t* __restrict__ q_out,
+                                                           uint16_t* __restrict__ k_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int heads = Hq + Hkv;
+  if (item >= (int64_t)T_ * heads) return;
+  const int64_t t = item / heads;
+  const int h = (int)(item % heads);
+  const bool is_q = h < Hq;
+  const uint16_t* src = qkv + t * row_stride + (int64_t)h * kD;
+  float x1 = to_float<T>(src[lane]);
+  float x2 = to_float<T>(src[lane + 64]);
+  if constexpr (kNorm) {
+    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)kD) + eps));
+    const uint16_t* w = is_q ? qw : kw;
+    x1 = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x1 * r)) * to_float<T>(w[lane])));
+    x2 = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x2 * r)) * to_float<T>(w[lane + 64])));
+  }
+  int64_t p = positions[t];
+  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const float c = cos_t[p * (kD / 2) + lane];
+  const float s = sin_t[p * (kD / 2) + lane];
+  const float y1 = x1 * c - x2 * s;
+  const float y2 = x2 * c + x1 * s;
+  uint16_t* dst = is_q ? q_out + (t * Hq + h) * kD : k_out + (t * Hkv + (h - Hq)) * kD;
+  dst[lane] = from_float<T>(y1);
+  dst[lane + 64] = from_float<T>(y2);
+}
+
+}  // namespace
+
+hipError_t launch_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positions, const float* cos_t,
+                               const float* sin_t, const void* q_weight, const void* k_weight, float eps, int64_t T_,
+                               int Hq, int Hkv, int max_pos, void* q_out, void* k_out, bool bf16,
+                               hipStream_t stream) {
+  const int64_t items = T_ * (Hq + Hkv);
+  const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+  auto X = static_cast<const uint16_t*>(qkv);
+  auto QW = static_cast<const uint16_t*>(q_weight);
+  auto KW = static_cast<const uint16_t*>(k_weight);
+  auto QO = static_cast<uint16_t*>(q_out);
+  auto KO = static_cast<uint16_t*>(k_out);
+  const bool norm = q_weight != nullptr;
+#define TVQ_ROPE(TT, NN)                                                                                       \
+  qk_norm_rope_kernel<TT, NN><<<grid, block, 0, stream>>>(X, row_stride, positions, cos_t, sin_t, QW, KW, eps, \
+                                                          (int)T_, Hq, Hkv, max_pos, QO, KO)
+  if (bf16) {
+    if (norm) TVQ_ROPE(BF16, true); else TVQ_ROPE(BF16, false);
+  } else {
+    if (norm) TVQ_ROPE(F16, true); else TVQ_ROPE(F16, false);
+  }
+#undef TVQ_ROPE
+  return hipGetLastError();
+}
+
+}  // namespace tvq

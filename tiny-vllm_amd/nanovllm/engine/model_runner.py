@@ -175,8 +175,15 @@ class ModelRunner:
                 ids.extend(s.token_ids)
                 pos.extend(range(len(s)))
                 cu.append(cu[-1] + len(s))
-            set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=max(len(s) for s in seqs),
-                        slot_mapping=torch.tensor([s.slot for s in seqs]))
+            lmax = max(len(s) for s in seqs)
+            if self.device == "cuda":
+                pad = [b * lmax + p for b, s in enumerate(seqs) for p in range(len(s))]
+                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax, num_seqs=len(seqs),
+                            slot_mapping=self._to_gpu([s.slot for s in seqs], torch.int64),
+                            pad_index=self._to_gpu(pad, torch.int64))
+            else:
+                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
+                            slot_mapping=torch.tensor([s.slot for s in seqs]))
             hidden = self.model(self._to_gpu(ids, torch.int64), self._to_gpu(pos, torch.int64))
             hidden = hidden[self._to_gpu(cu[1:], torch.int64) - 1]
         elif self.graphs and len(seqs) <= self.graph_bs[-1]:

@@ -78,13 +78,39 @@ class Attention(nn.Module):
         self.scale = head_dim ** -0.5
         self.k_cache = self.v_cache = None  # set by the engine
 
+    def _prefill_padded(self, q, k, v, ctx) -> torch.Tensor:
+        """All prompts of the step in one SDPA call: tokens are scattered into
+        a zero-padded [B, L, H, D] batch (pad_index). Right padding with
+        is_causal=True keeps every real query on real keys only. The keys and
+        values of each sequence are stored into its cache slot in the same
+        batched copy (positions past a sequence's length receive padding,
+        which decode overwrites before it ever reads them)."""
+        b, length = ctx.num_seqs, int(ctx.max_seqlen_q)
+        idx = ctx.pad_index
+        group = self.num_heads // self.num_kv_heads
+
+        def pad(t):
+            return t.new_zeros((b * length,) + tuple(t.shape[1:])).index_copy_(0, idx, t).view(b, length, *t.shape[1:])
+
+        qp, kp, vp = pad(q), pad(k), pad(v)
+        if self.k_cache is not None and ctx.slot_mapping is not None:
+            self.k_cache[ctx.slot_mapping, :, :length] = kp.transpose(1, 2)
+            self.v_cache[ctx.slot_mapping, :, :length] = vp.transpose(1, 2)
+        if group > 1:
+            kp, vp = kp.repeat_interleave(group, 2), vp.repeat_interleave(group, 2)
+        o = F.scaled_dot_product_attention(qp.transpose(1, 2), kp.transpose(1, 2), vp.transpose(1, 2),
+                                           is_causal=True, scale=self.scale)   # [B, H, L, D]
+        return o.transpose(1, 2).reshape(b * length, self.num_heads, self.head_dim).index_select(0, idx)
+
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         ctx = get_context()
         group = self.num_heads // self.num_kv_heads
         if ctx.is_prefill:
-            # Ragged prefill: one causal attention per sequence (host-side
-            # cu_seqlens_q), after writing its keys/values to its cache slot.
-            # K/V heads are expanded so SDPA can take its fused kernels.
+            if q.is_cuda:
+                return self._prefill_padded(q, k, v, ctx)
+            # Host path (CPU tests): one causal attention per sequence
+            # (host-side cu_seqlens_q), after writing its keys/values to its
+            # cache slot.
             out = torch.empty_like(q)
             cu = ctx.cu_seqlens_q.tolist()
             slots = ctx.slot_mapping.tolist() if ctx.slot_mapping is not None else [None] * (len(cu) - 1)
@@ -151,15 +177,24 @@ class Qwen3Attention(nn.Module):
             self.q_norm = RMSNorm(cfg.head_dim, cfg.rms_norm_eps)
             self.k_norm = RMSNorm(cfg.head_dim, cfg.rms_norm_eps)
 
-    def forward(self, positions: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, positions: torch.Tensor, x) -> torch.Tensor:
         qkv = self.qkv_proj(x)
-        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = q.reshape(-1, self.num_heads, self.head_dim)
-        k = k.reshape(-1, self.num_kv_heads, self.head_dim)
-        v = v.reshape(-1, self.num_kv_heads, self.head_dim)
-        if self.qk_norm:
-            q, k = self.q_norm(q), self.k_norm(k)
-        q, k = self.rotary_emb(positions, q, k)
+        if qkv.is_cuda:
+            # fused per-head q/k RMSNorm + rotary (one HIP launch); v stays a view
+            qw = self.q_norm.weight if self.qk_norm else None
+            kw = self.k_norm.weight if self.qk_norm else None
+            eps = self.q_norm.eps if self.qk_norm else 0.0
+            q, k = _hip.qk_norm_rope(qkv, positions, self.rotary_emb.cos, self.rotary_emb.sin, qw, kw, eps,
+                                     self.num_heads, self.num_kv_heads, self.head_dim)
+            v = qkv[:, self.q_size + self.kv_size:].view(-1, self.num_kv_heads, self.head_dim)
+        else:
+            q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+            q = q.reshape(-1, self.num_heads, self.head_dim)
+            k = k.reshape(-1, self.num_kv_heads, self.head_dim)
+            v = v.reshape(-1, self.num_kv_heads, self.head_dim)
+            if self.qk_norm:
+                q, k = self.q_norm(q), self.k_norm(k)
+            q, k = self.rotary_emb(positions, q, k)
         o = self.attn(q, k, v)
         return self.o_proj(o.reshape(-1, self.q_size))
 

@@ -43,6 +43,8 @@ SYMBOLS = (
     ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP)),
     ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
+    ("tvq_qk_norm_rope", _INT, (_VP, _I64, _VP, _VP, _VP, _VP, _VP, ctypes.c_float, _I64, _INT, _INT, _INT, _I64,
+                                _VP, _VP, _INT, _VP)),
     ("tvq_decode_attention", _INT, (_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _INT, _INT, _INT, _I64,
                                     _I64, ctypes.c_float, _VP, _INT, _VP)),
 )
@@ -330,3 +332,34 @@ def decode_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, 
                                       _TORCH_TO_TVQ[q.dtype], _stream(dev))
     _check(rc, "tvq_decode_attention")
     return out
+
+
+def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                 q_weight: torch.Tensor | None, k_weight: torch.Tensor | None, eps: float, num_heads: int,
+                 num_kv_heads: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """q/k of a packed qkv [T, >= (Hq+Hkv)*D] (row-contiguous): per-head
+    RMSNorm (when weights are given) and rotate-half rotary embedding.
+    Returns q [T, Hq, D], k [T, Hkv, D]."""
+    lib = load_library()
+    dev = qkv.device
+    _require(qkv.is_cuda and qkv.dim() == 2 and qkv.stride(1) == 1, "qkv must be a row-contiguous 2-D GPU tensor")
+    _require(qkv.dtype in _TORCH_TO_TVQ, "qkv must be float16 or bfloat16")
+    _require(positions.is_cuda and positions.dtype == torch.int64 and positions.is_contiguous(),
+             "positions must be contiguous int64 on the GPU")
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32 and cos.is_contiguous() and
+             sin.is_contiguous() and cos.shape == sin.shape and cos.shape[1] == head_dim // 2,
+             "cos / sin must be contiguous fp32 [max_pos, head_dim/2]")
+    for w in (q_weight, k_weight):
+        _require(w is None or (w.dtype == qkv.dtype and w.is_contiguous() and w.numel() == head_dim),
+                 "norm weights must be contiguous [head_dim] of qkv's dtype")
+    t = qkv.shape[0]
+    q = torch.empty((t, num_heads, head_dim), dtype=qkv.dtype, device=dev)
+    k = torch.empty((t, num_kv_heads, head_dim), dtype=qkv.dtype, device=dev)
+    if t == 0:
+        return q, k
+    with torch.cuda.device(dev):
+        rc = lib.tvq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                  _ptr(q_weight), _ptr(k_weight), eps, t, num_heads, num_kv_heads, head_dim,
+                                  cos.shape[0], q.data_ptr(), k.data_ptr(), _TORCH_TO_TVQ[qkv.dtype], _stream(dev))
+    _check(rc, "tvq_qk_norm_rope")
+    return q, k

@@ -20,6 +20,10 @@ class Context:
     block_tables: torch.Tensor | None = None
     kv_lo: int = 0   # decode: KV-cache slot range of the running batch
     kv_hi: int = 0
+    # prefill on the GPU: sequences padded to [batch, max_seqlen_q]; token t
+    # of the packed batch sits at row pad_index[t] = b * max_seqlen_q + pos
+    pad_index: torch.Tensor | None = None
+    num_seqs: int = 0
 
 
 _CONTEXT = Context()
@@ -30,10 +34,10 @@ def get_context() -> Context:
 
 
 def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0, slot_mapping=None,
-                context_lens=None, block_tables=None, kv_lo=0, kv_hi=0) -> None:
+                context_lens=None, block_tables=None, kv_lo=0, kv_hi=0, pad_index=None, num_seqs=0) -> None:
     global _CONTEXT
     _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, slot_mapping,
-                       context_lens, block_tables, kv_lo, kv_hi)
+                       context_lens, block_tables, kv_lo, kv_hi, pad_index, num_seqs)
 
 
 def reset_context() -> None:
