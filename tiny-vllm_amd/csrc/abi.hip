@@ -70,12 +70,16 @@ int run_gemm(const GemmArgs& a, void* stream) {
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
   if (!aligned) return Path::kGeneric;
-  if (a.M <= kSkinnyMaxM) return stream_shape_ok(a.M, a.N, a.K) ? Path::kStream : Path::kSkinny;
+  if (a.M <= kSkinnyMaxM) {
+    if (a.M > kDmaMinM && dma_shape_ok(a.K)) return Path::kDma;
+    return stream_shape_ok(a.M, a.N, a.K) ? Path::kStream : Path::kSkinny;
+  }
   return dma_shape_ok(a.K) ? Path::kDma : Path::kTiled;
 }
 
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
+  if (M > kDmaMinM && dma_shape_ok(K)) return dma_path_name(w8a8, M, N);
   if (M <= kSkinnyMaxM && stream_shape_ok(M, N, K)) {
     static const char* s8[4] = {"stream_mfma_i8_m16", "stream_mfma_i8_m32", "stream_mfma_i8_m48", "stream_mfma_i8_m64"};
     static const char* s16[4] = {"stream_mfma_f16x_m16", "stream_mfma_f16x_m32", "stream_mfma_f16x_m48",

@@ -57,7 +57,9 @@ const char* dma_path_name(bool w8a8, int64_t M, int64_t N);
 hipError_t launch_stream(const GemmArgs& a, hipStream_t stream);
 bool stream_shape_ok(int64_t M, int64_t N, int64_t K);
 
-// Largest M served by the skinny / stream families.
+// Largest M served by the skinny / stream families; above kDmaMinM they are
+// used only when K % 128 != 0 (the DMA tiles need whole 128-k stages).
 constexpr int64_t kSkinnyMaxM = 64;
+constexpr int64_t kDmaMinM = 16;
 
 }  // namespace tvq
