@@ -19,16 +19,16 @@
 // Any consistent assignment of k to (lane group, register slot) yields the
 // same dot products, so A and B only have to agree with each other.
 //
-// A 256-thread workgroup owns 16*RG output channels; its 4 waves split K in
-// interleaved runs of U 64-wide chunks and are reduced through LDS at the
-// end, so the whole reduction order is fixed (deterministic output).
+// A workgroup of W waves (W = 4, 8 or 16, chosen so that each wave needs about
+// one run over K) owns 16*RG output channels; its waves split K in interleaved
+// runs of U 64-wide chunks and are reduced through LDS at the end in a fixed
+// order (deterministic output). More waves per row group means more weight
+// loads in flight per workgroup and shorter latency chains per wave.
 #include "tvq_common.h"
 #include "tvq_internal.h"
 
 namespace tvq {
 namespace {
-
-constexpr int kWaves = 4;
 
 template <int MG, int RG>
 struct SkinnyCfg {
@@ -37,8 +37,8 @@ struct SkinnyCfg {
   static constexpr int U = (8 / (RG * MG)) > 0 ? (8 / (RG * MG)) : 1;
 };
 
-template <typename T, bool kW8A8, bool kRaw, int MG, int RG>
-__global__ __launch_bounds__(256) void skinny_kernel(const void* __restrict__ xv, const float* __restrict__ a_scales,
+template <typename T, bool kW8A8, bool kRaw, int MG, int RG, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restrict__ xv, const float* __restrict__ a_scales,
                                                      const int8_t* __restrict__ qw, const float* __restrict__ ws,
                                                      const uint16_t* __restrict__ bias, void* __restrict__ yv,
                                                      int M, int N, int K) {
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(const void* __restrict__ xv
   __syncthreads();
 
   constexpr int kItems = RG * MG * 64;
-  for (int it = tid; it < kItems; it += 256) {
+  for (int it = tid; it < kItems; it += 64 * kWaves) {
     const int ij = it >> 6;
     const int ln = it & 63;
     const int i = ij / MG;
@@ -174,21 +174,36 @@ __global__ __launch_bounds__(256) void skinny_kernel(const void* __restrict__ xv
   }
 }
 
+template <typename T, bool kW8A8, bool kRaw, int MG, int RG, int W>
+hipError_t launch_w(const GemmArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.N + 16 * RG - 1) / (16 * RG)));
+  const dim3 block(64 * W);
+  skinny_kernel<T, kW8A8, kRaw, MG, RG, W><<<grid, block, 0, stream>>>(
+      a.x, a.a_scales, a.qweight, a.scales, static_cast<const uint16_t*>(a.bias), a.y, (int)a.M, (int)a.N, (int)a.K);
+  return hipGetLastError();
+}
+
+template <typename T, bool kW8A8, bool kRaw, int MG, int RG>
+hipError_t launch_rg(const GemmArgs& a, hipStream_t stream) {
+  // Waves per workgroup: enough that each wave needs about one run of U
+  // chunks over K (at least 4; 16 or 8 only while the LDS reduction buffer,
+  // W x RG x MG KB, stays within 32 KB).
+  constexpr int U = SkinnyCfg<MG, RG>::U;
+  const int64_t runs = (a.K + 64 * U - 1) / (64 * U);
+  if constexpr (RG * MG <= 2) {
+    if (runs > 8) return launch_w<T, kW8A8, kRaw, MG, RG, 16>(a, stream);
+  }
+  if constexpr (RG * MG <= 4) {
+    if (runs > 4) return launch_w<T, kW8A8, kRaw, MG, RG, 8>(a, stream);
+  }
+  return launch_w<T, kW8A8, kRaw, MG, RG, 4>(a, stream);
+}
+
 template <typename T, bool kW8A8, bool kRaw, int MG>
 hipError_t launch_mg(const GemmArgs& a, hipStream_t stream) {
   // Two row groups per wave only when that still leaves >= 4 workgroups per CU.
-  const bool rg2 = a.N >= 16 * 2 * 1024;
-  const int rows = rg2 ? 32 : 16;
-  const dim3 grid((unsigned)((a.N + rows - 1) / rows));
-  const dim3 block(256);
-  const uint16_t* bias = static_cast<const uint16_t*>(a.bias);
-  if (rg2)
-    skinny_kernel<T, kW8A8, kRaw, MG, 2><<<grid, block, 0, stream>>>(a.x, a.a_scales, a.qweight, a.scales, bias, a.y,
-                                                                       (int)a.M, (int)a.N, (int)a.K);
-  else
-    skinny_kernel<T, kW8A8, kRaw, MG, 1><<<grid, block, 0, stream>>>(a.x, a.a_scales, a.qweight, a.scales, bias, a.y,
-                                                                       (int)a.M, (int)a.N, (int)a.K);
-  return hipGetLastError();
+  if (a.N >= 16 * 2 * 1024) return launch_rg<T, kW8A8, kRaw, MG, 2>(a, stream);
+  return launch_rg<T, kW8A8, kRaw, MG, 1>(a, stream);
 }
 
 template <typename T, bool kW8A8, bool kRaw>
