@@ -183,6 +183,23 @@ int tvq_qk_norm_rope(const void* qkv, int64_t row_stride,
                      int Hkv, int head_dim, int64_t max_pos, void* q_out,
                      void* k_out, int dtype, void* stream);
 
+/* Causal attention over the packed prompts of a prefill step (no cached
+ * prefix). Replaces flash_attn_varlen_func(q, k, v, cu_seqlens..., causal=True)
+ * in the prefill branch of Attention.forward (nanovllm/layers/attention.py:75-84).
+ *   q [T, Hq, head_dim], k [T, Hkv, head_dim]   contiguous, packed tokens
+ *   v [T, ...]  row stride v_stride elements, heads contiguous (head_dim each)
+ *   blocks [nblocks, 3] int32: (token offset of the sequence, its length,
+ *          first query of a 64-query block), one row per query block
+ *   out [T, Hq, head_dim] contiguous
+ * out[t, h] = softmax(scale * q[t,h] . K_seq[0..pos]) V_seq[0..pos] over the
+ * sequence's own keys up to its position (kv head h / (Hq/Hkv)). fp32 math;
+ * the probabilities are rounded to `dtype` for the value product. head_dim
+ * must be 128, Hq/Hkv an integer, pointers 16-byte aligned. */
+int tvq_prefill_attention(const void* q, const void* k, const void* v,
+                          int64_t v_stride, const int32_t* blocks,
+                          int64_t nblocks, int Hq, int Hkv, int head_dim,
+                          float scale, void* out, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,3 +100,46 @@ def test_decode_attention_in_graph_replays(hiplib):
         ref = _hip.decode_attention(q, k, v, kc.clone(), vc.clone(), slots, lens, 0.088)
         torch.cuda.synchronize()
         assert torch.equal(got, ref)
+
+
+def _prefill_ref(q, k, v, lens, scale):
+    out = torch.empty_like(q, dtype=torch.float32)
+    hq, hkv = q.shape[1], k.shape[1]
+    off = 0
+    for n in lens:
+        qq = q[off:off + n].float().transpose(0, 1)                                # [Hq, n, D]
+        kk = k[off:off + n].float().transpose(0, 1).repeat_interleave(hq // hkv, 0)
+        vv = v[off:off + n].float().transpose(0, 1).repeat_interleave(hq // hkv, 0)
+        s = qq @ kk.transpose(1, 2) * scale
+        s.masked_fill_(torch.ones(n, n, dtype=torch.bool, device=q.device).triu(1), float("-inf"))
+        out[off:off + n] = (torch.softmax(s, -1) @ vv).transpose(0, 1)
+        off += n
+    return out
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_attention_matches_fp32_reference(hiplib, hq, hkv, dtype):
+    from nanovllm.quantization import _hip
+    print(f"CASE prefill_attention hq={hq} hkv={hkv} dtype={dtype}", flush=True)
+    lens = [1, 5, 64, 65, 100, 300, 1024, 17]
+    t, d = sum(lens), 128
+    g = torch.Generator(device="cuda").manual_seed(hq + hkv)
+    q = torch.randn(t, hq, d, device="cuda", generator=g).to(dtype)
+    k = torch.randn(t, hkv, d, device="cuda", generator=g).to(dtype)
+    qkv = torch.randn(t, (hq + 2 * hkv) * d, device="cuda", generator=g).to(dtype)
+    v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)          # strided view, as the model passes it
+    offs, o = [], 0
+    for n in lens:
+        offs.append((o, n))
+        o += n
+    blocks = _hip.prefill_blocks(offs).cuda()
+    scale = d ** -0.5
+    out = _hip.prefill_attention(q, k, v, blocks, scale)
+    torch.cuda.synchronize()
+    ref = _prefill_ref(q, k, v, lens, scale)
+    err = (out.float() - ref).abs()
+    # P is rounded to the input dtype before the value product (as flash attention does)
+    tol = (1.5e-2 if dtype == torch.bfloat16 else 4e-3) * ref.abs().amax() + 1e-3
+    assert err.max().item() <= tol, (err.max().item(), tol)
+    assert ((out.float() - ref).norm() / ref.norm()).item() < (8e-3 if dtype == torch.bfloat16 else 2e-3)

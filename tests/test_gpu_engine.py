@@ -40,8 +40,8 @@ def _prefill_logits(model, ids: list[int], device) -> torch.Tensor:
     """Cache-free prefill of one sequence (no KV slot written)."""
     n = len(ids)
     if device == "cuda":
-        set_context(True, cu_seqlens_q=torch.tensor([0, n]), max_seqlen_q=n, num_seqs=1, slot_mapping=None,
-                    pad_index=torch.arange(n, device="cuda"))
+        set_context(True, cu_seqlens_q=torch.tensor([0, n]), max_seqlen_q=n, slot_mapping=None,
+                    attn_blocks=_hip.prefill_blocks([(0, n)]).cuda())
     else:
         set_context(True, cu_seqlens_q=torch.tensor([0, n]), slot_mapping=None)
     with torch.no_grad():

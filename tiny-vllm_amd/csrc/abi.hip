@@ -240,4 +240,21 @@ int tvq_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positio
   return ok();
 }
 
+int tvq_prefill_attention(const void* q, const void* k, const void* v, int64_t v_stride, const int32_t* blocks,
+                          int64_t nblocks, int Hq, int Hkv, int head_dim, float scale, void* out, int dtype,
+                          void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (nblocks < 0 || nblocks > kMaxDim) return fail(TVQ_E_INVALID, "invalid nblocks");
+  if (nblocks == 0) return ok();
+  if (!q || !k || !v || !blocks || !out) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (head_dim != 128) return fail(TVQ_E_UNSUPPORTED, "head_dim must be 128, got %d", head_dim);
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || Hq > 65535) return fail(TVQ_E_INVALID, "invalid Hq / Hkv");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || v_stride % 8)
+    return fail(TVQ_E_UNSUPPORTED, "prefill attention needs 16-byte aligned pointers and strides");
+  hipError_t e = launch_prefill_attention(q, k, v, v_stride, blocks, (int)nblocks, Hq, Hkv, scale, out,
+                                          dtype == TVQ_DTYPE_BF16, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "prefill attention launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

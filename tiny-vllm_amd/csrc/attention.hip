@@ -189,4 +189,188 @@ hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* 
                               max_len, num_slots, scale, out, stream);
 }
 
+
+// ---------------------------------------------------------------------------
+// Prefill (varlen, causal) attention.
+//
+// Replaces the prefill branch of Attention.forward
+// (nanovllm/layers/attention.py:75-84: flash_attn_varlen_func(q, k, v,
+// cu_seqlens, causal=True)) for prompts without a cached prefix. q, k, v are
+// the packed new tokens of all sequences; a host-built block table lists the
+// 64-query blocks (token offset of the sequence, its length, first query of
+// the block), longest work first.
+//
+// One 256-thread workgroup per (query block, query head): each wave owns 16
+// queries; 64-key blocks of K and V (the kv head of the query head) are
+// staged in LDS, K row-major and V transposed. Both products run on
+// v_mfma_f32_16x16x32_bf16 in transposed form so no data moves between them:
+//   S^T[key][q] = K[key][:] . Q[q][:]          (A = K rows, B = Q rows)
+//   O^T[d][q]  += V^T[d][keys] . P^T[keys][q]  (B = P^T straight from the
+//                                               S^T accumulators)
+// The MFMA k-dimension may be permuted as long as A and B agree, so lane
+// group g feeds keys {4g..4g+3, 16+4g..16+4g+3} of each 32-key chunk: exactly
+// the keys its S^T accumulators hold. Softmax statistics are per query = per
+// lane column; the online rescale is lane-local. fp32 accumulation, exp2 with
+// the scale folded into log2(e), P rounded to the input dtype for the second
+// product (as flash attention does).
+namespace {
+
+constexpr int kBlkQ = 64;
+constexpr int kBlkK = 64;
+constexpr int kKStride = kD + 8;      // K tile row stride (elements): 16-row fragment reads hit distinct banks
+constexpr int kVtStride = kBlkK + 4;  // V^T tile row stride (elements)
+
+template <typename T>
+__global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __restrict__ q,
+                                                           const uint16_t* __restrict__ k,
+                                                           const uint16_t* __restrict__ v, int64_t v_stride,
+                                                           const int32_t* __restrict__ blocks, int Hq, int Hkv,
+                                                           float scale_log2, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kBlkK * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kVtStride];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int r = lane & 15;
+  const int h = blockIdx.y;
+  const int hk = h / (Hq / Hkv);
+  const int64_t seq0 = blocks[3 * blockIdx.x];      // token offset of the sequence
+  const int len = blocks[3 * blockIdx.x + 1];
+  const int q0 = blocks[3 * blockIdx.x + 2];         // first query of the block (within the sequence)
+
+  // this lane's query (B operand rows of S^T, C columns of both products)
+  const int qi = q0 + wave * 16 + r;
+  const int qc = min(qi, len - 1);
+  u32x4 qf[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    qf[c] = *reinterpret_cast<const u32x4*>(q + ((seq0 + qc) * Hq + h) * kD + 32 * c + 8 * g);
+
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  const int kv_end = min(len, q0 + kBlkQ);           // causal: keys < last query of the block + 1
+  for (int kv0 = 0; kv0 < kv_end; kv0 += kBlkK) {
+    __syncthreads();  // previous block's tiles are no longer read
+    {
+      // K tile: thread -> key tid/4, 64-byte quarter tid%4 (coalesced rows)
+      const int key = tid >> 2, part = tid & 3;
+      const int kc = min(kv0 + key, len - 1);
+      const uint16_t* src = k + ((seq0 + kc) * Hkv + hk) * kD + 32 * part;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<u32x4*>(&ks[key * kKStride + 32 * part + 8 * j]) =
+            *reinterpret_cast<const u32x4*>(src + 8 * j);
+      // V tile, transposed: thread -> key tid%64, dims 32*(tid/64) .. +32
+      const int vkey = tid & 63, dg = tid >> 6;
+      const int vc = min(kv0 + vkey, len - 1);
+      const uint16_t* vsrc = v + (seq0 + vc) * v_stride + hk * kD + 32 * dg;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(vsrc + 8 * j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          vt[(32 * dg + 8 * j + e) * kVtStride + vkey] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+    __syncthreads();
+
+    // S^T tiles: 4 x (16 keys x 16 queries), k = head dim in 4 chunks of 32
+    f32x4 s[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[(kt * 16 + r) * kKStride + 32 * c + 8 * g]);
+        acc = mfma16x16x32<T>(a, qf[c], acc);
+      }
+      s[kt] = acc;
+    }
+    // scale, causal + length mask, block max per query (lane column r)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int key = kv0 + kt * 16 + 4 * g + t;
+        const float sv = (key <= qi && key < len) ? s[kt][t] * scale_log2 : -INFINITY;
+        s[kt][t] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float mn = fmaxf(m, mx);  // finite: key 0 is valid for every query
+    const float corr = exp2f(m - mn);
+    float ps = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float p = exp2f(s[kt][t] - mn);
+        s[kt][t] = p;
+        ps += p;
+      }
+    ps += __shfl_xor(ps, 16, kWave);
+    ps += __shfl_xor(ps, 32, kWave);
+    l = l * corr + ps;
+    m = mn;
+    // P^T as the B operand: chunk c holds keys {4g..4g+3} of tiles 2c and 2c+1
+    u32x4 pb[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      pb[c][0] = (uint32_t)from_float<T>(s[2 * c][0]) | ((uint32_t)from_float<T>(s[2 * c][1]) << 16);
+      pb[c][1] = (uint32_t)from_float<T>(s[2 * c][2]) | ((uint32_t)from_float<T>(s[2 * c][3]) << 16);
+      pb[c][2] = (uint32_t)from_float<T>(s[2 * c + 1][0]) | ((uint32_t)from_float<T>(s[2 * c + 1][1]) << 16);
+      pb[c][3] = (uint32_t)from_float<T>(s[2 * c + 1][2]) | ((uint32_t)from_float<T>(s[2 * c + 1][3]) << 16);
+    }
+    // O^T tiles: 8 x (16 dims x 16 queries), k = 64 keys in 2 chunks
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x4 acc = o[dt] * corr;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint16_t* row = &vt[(16 * dt + r) * kVtStride + 32 * c + 4 * g];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+        acc = mfma16x16x32<T>(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c], acc);
+      }
+      o[dt] = acc;
+    }
+  }
+
+  if (qi < len) {
+    const float inv = 1.0f / l;
+    uint16_t* dst = out + ((seq0 + qi) * Hq + h) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      u32x2 pk;
+      pk.x = (uint32_t)from_float<T>(o[dt][0] * inv) | ((uint32_t)from_float<T>(o[dt][1] * inv) << 16);
+      pk.y = (uint32_t)from_float<T>(o[dt][2] * inv) | ((uint32_t)from_float<T>(o[dt][3] * inv) << 16);
+      *reinterpret_cast<u32x2*>(dst + 16 * dt + 4 * g) = pk;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_prefill_attention(const void* q, const void* k, const void* v, int64_t v_stride,
+                                    const int32_t* blocks, int nblocks, int Hq, int Hkv, float scale, void* out,
+                                    bool bf16, hipStream_t stream) {
+  const dim3 grid((unsigned)nblocks, (unsigned)Hq), block(256);
+  const float sl2 = scale * 1.4426950408889634f;  // log2(e)
+  auto Q = static_cast<const uint16_t*>(q);
+  auto Kp = static_cast<const uint16_t*>(k);
+  auto V = static_cast<const uint16_t*>(v);
+  auto O = static_cast<uint16_t*>(out);
+  if (bf16)
+    prefill_attn_kernel<BF16><<<grid, block, 0, stream>>>(Q, Kp, V, v_stride, blocks, Hq, Hkv, sl2, O);
+  else
+    prefill_attn_kernel<F16><<<grid, block, 0, stream>>>(Q, Kp, V, v_stride, blocks, Hq, Hkv, sl2, O);
+  return hipGetLastError();
+}
+
 }  // namespace tvq

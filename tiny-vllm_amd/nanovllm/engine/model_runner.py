@@ -30,6 +30,7 @@ from nanovllm.config import Config
 from nanovllm.engine.sequence import Sequence
 from nanovllm.layers.linear import LinearBase
 from nanovllm.models.qwen3 import Attention, Qwen3ForCausalLM, RMSNorm
+from nanovllm.quantization import _hip
 from nanovllm.quantization.utils import quantize_int8_per_channel
 from nanovllm.utils.context import reset_context, set_context
 from nanovllm.utils.loader import load_model
@@ -177,10 +178,12 @@ class ModelRunner:
                 cu.append(cu[-1] + len(s))
             lmax = max(len(s) for s in seqs)
             if self.device == "cuda":
-                pad = [b * lmax + p for b, s in enumerate(seqs) for p in range(len(s))]
-                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax, num_seqs=len(seqs),
+                blocks = _hip.prefill_blocks([(cu[i], len(s)) for i, s in enumerate(seqs)])
+                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
                             slot_mapping=self._to_gpu([s.slot for s in seqs], torch.int64),
-                            pad_index=self._to_gpu(pad, torch.int64))
+                            attn_blocks=blocks.pin_memory().cuda(non_blocking=True),
+                            token_slots=self._to_gpu([s.slot for s in seqs for _ in range(len(s))], torch.int64),
+                            token_pos=self._to_gpu(pos, torch.int64))
             else:
                 set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
                             slot_mapping=torch.tensor([s.slot for s in seqs]))

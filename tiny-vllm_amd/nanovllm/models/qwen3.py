@@ -78,36 +78,21 @@ class Attention(nn.Module):
         self.scale = head_dim ** -0.5
         self.k_cache = self.v_cache = None  # set by the engine
 
-    def _prefill_padded(self, q, k, v, ctx) -> torch.Tensor:
-        """All prompts of the step in one SDPA call: tokens are scattered into
-        a zero-padded [B, L, H, D] batch (pad_index). Right padding with
-        is_causal=True keeps every real query on real keys only. The keys and
-        values of each sequence are stored into its cache slot in the same
-        batched copy (positions past a sequence's length receive padding,
-        which decode overwrites before it ever reads them)."""
-        b, length = ctx.num_seqs, int(ctx.max_seqlen_q)
-        idx = ctx.pad_index
-        group = self.num_heads // self.num_kv_heads
-
-        def pad(t):
-            return t.new_zeros((b * length,) + tuple(t.shape[1:])).index_copy_(0, idx, t).view(b, length, *t.shape[1:])
-
-        qp, kp, vp = pad(q), pad(k), pad(v)
-        if self.k_cache is not None and ctx.slot_mapping is not None:
-            self.k_cache[ctx.slot_mapping, :, :length] = kp.transpose(1, 2)
-            self.v_cache[ctx.slot_mapping, :, :length] = vp.transpose(1, 2)
-        if group > 1:
-            kp, vp = kp.repeat_interleave(group, 2), vp.repeat_interleave(group, 2)
-        o = F.scaled_dot_product_attention(qp.transpose(1, 2), kp.transpose(1, 2), vp.transpose(1, 2),
-                                           is_causal=True, scale=self.scale)   # [B, H, L, D]
-        return o.transpose(1, 2).reshape(b * length, self.num_heads, self.head_dim).index_select(0, idx)
+    def _prefill_gpu(self, q, k, v, ctx) -> torch.Tensor:
+        """Store every prompt token's K/V at (its sequence's slot, its
+        position) in one batched copy, then run the HIP varlen causal
+        attention over the packed prompts."""
+        if self.k_cache is not None and ctx.token_slots is not None:
+            self.k_cache[ctx.token_slots, :, ctx.token_pos] = k
+            self.v_cache[ctx.token_slots, :, ctx.token_pos] = v
+        return _hip.prefill_attention(q, k, v, ctx.attn_blocks, self.scale)
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         ctx = get_context()
         group = self.num_heads // self.num_kv_heads
         if ctx.is_prefill:
             if q.is_cuda:
-                return self._prefill_padded(q, k, v, ctx)
+                return self._prefill_gpu(q, k, v, ctx)
             # Host path (CPU tests): one causal attention per sequence
             # (host-side cu_seqlens_q), after writing its keys/values to its
             # cache slot.

@@ -45,6 +45,8 @@ SYMBOLS = (
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_qk_norm_rope", _INT, (_VP, _I64, _VP, _VP, _VP, _VP, _VP, ctypes.c_float, _I64, _INT, _INT, _INT, _I64,
                                 _VP, _VP, _INT, _VP)),
+    ("tvq_prefill_attention", _INT, (_VP, _VP, _VP, _I64, _VP, _I64, _INT, _INT, _INT, ctypes.c_float, _VP, _INT,
+                                     _VP)),
     ("tvq_decode_attention", _INT, (_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _INT, _INT, _INT, _I64,
                                     _I64, ctypes.c_float, _VP, _INT, _VP)),
 )
@@ -363,3 +365,37 @@ def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, 
                                   cos.shape[0], q.data_ptr(), k.data_ptr(), _TORCH_TO_TVQ[qkv.dtype], _stream(dev))
     _check(rc, "tvq_qk_norm_rope")
     return q, k
+
+
+def prefill_blocks(offsets_lens: list[tuple[int, int]], block_q: int = 64) -> torch.Tensor:
+    """Host-side block table for prefill_attention: one (token offset,
+    length, first query) row per 64-query block, blocks with the most keys
+    first (they take longest)."""
+    rows = [(off, n, q0) for off, n in offsets_lens for q0 in range(0, n, block_q)]
+    rows.sort(key=lambda x: -x[2])
+    return torch.tensor(rows, dtype=torch.int32).reshape(-1, 3)
+
+
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, blocks: torch.Tensor,
+                      scale: float) -> torch.Tensor:
+    """Causal attention of packed prompts: q [T, Hq, D], k [T, Hkv, D]
+    contiguous, v [T, Hkv, D] with contiguous heads (token stride free);
+    blocks from prefill_blocks, on the GPU."""
+    lib = load_library()
+    dev = q.device
+    _require(q.is_cuda and q.is_contiguous() and k.is_contiguous(), "q and k must be contiguous GPU tensors")
+    _require(v.is_cuda and v.dim() == 3 and v.stride(2) == 1 and v.stride(1) == v.shape[2],
+             "v must be [T, Hkv, D] with contiguous heads")
+    _require(blocks.is_cuda and blocks.dtype == torch.int32 and blocks.is_contiguous() and blocks.dim() == 2,
+             "blocks must be a contiguous int32 [n, 3] GPU tensor")
+    _require(q.dtype in _TORCH_TO_TVQ and k.dtype == q.dtype and v.dtype == q.dtype, "dtype mismatch")
+    t, hq, d = q.shape
+    out = torch.empty_like(q)
+    if blocks.shape[0] == 0:
+        return out
+    with torch.cuda.device(dev):
+        rc = lib.tvq_prefill_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0), blocks.data_ptr(),
+                                       blocks.shape[0], hq, k.shape[1], d, scale, out.data_ptr(),
+                                       _TORCH_TO_TVQ[q.dtype], _stream(dev))
+    _check(rc, "tvq_prefill_attention")
+    return out
