@@ -61,3 +61,34 @@ def test_qk_norm_rope(hiplib, norm, dtype, t, hq, hkv):
         head_ulp = rf.abs().amax(-1, keepdim=True) * 2.0 ** (-7 if dtype == torch.bfloat16 else -10)
         assert torch.all((gf - rf).abs() <= 2.0001 * ulp + head_ulp + 1e-6)
         assert (gf == rf).float().mean() >= 0.99
+
+
+def test_qk_norm_rope_stores_prompt_kv(hiplib):
+    """With caches given, every token's rotated key and its value land at
+    (slot, position); tokens with an out-of-range slot or position are not
+    stored and nothing else in the caches changes."""
+    from nanovllm.quantization import _hip
+    t, hq, hkv, d, n_slots, max_len = 40, 16, 8, 128, 5, 64
+    g = torch.Generator(device="cuda").manual_seed(7)
+    qkv = torch.randn(t, (hq + 2 * hkv) * d, device="cuda", generator=g).bfloat16()
+    pos = torch.cat([torch.arange(20), torch.arange(17), torch.tensor([63, 64, 5])]).cuda()
+    slots = torch.tensor([3] * 20 + [0] * 17 + [4, 4, 9], dtype=torch.int64, device="cuda")
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float) / d))
+    fr = torch.outer(torch.arange(128, dtype=torch.float), inv)
+    cos, sin = fr.cos().cuda(), fr.sin().cuda()
+    w = torch.ones(d, device="cuda").bfloat16()
+    kc = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).bfloat16()
+    vc = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).bfloat16()
+    kc0, vc0 = kc.clone(), vc.clone()
+    q, k = _hip.qk_norm_rope(qkv, pos, cos, sin, w, w, 1e-6, hq, hkv, d, kc, vc, slots)
+    q2, k2 = _hip.qk_norm_rope(qkv, pos, cos, sin, w, w, 1e-6, hq, hkv, d)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(k, k2)
+    v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    ek, ev = kc0.clone(), vc0.clone()
+    for i in range(t):
+        s, p = int(slots[i]), int(pos[i])
+        if 0 <= s < n_slots and 0 <= p < max_len:
+            ek[s, :, p] = k[i]
+            ev[s, :, p] = v[i]
+    assert torch.equal(kc, ek) and torch.equal(vc, ev)

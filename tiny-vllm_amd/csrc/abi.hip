@@ -224,7 +224,8 @@ int tvq_decode_attention(const void* q, int64_t q_stride, const void* k_new, int
 
 int tvq_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positions, const float* cos_t,
                      const float* sin_t, const void* q_weight, const void* k_weight, float eps, int64_t T, int Hq,
-                     int Hkv, int head_dim, int64_t max_pos, void* q_out, void* k_out, int dtype, void* stream) {
+                     int Hkv, int head_dim, int64_t max_pos, void* q_out, void* k_out, void* k_cache, void* v_cache,
+                     const int64_t* slots, int64_t num_slots, int64_t max_len, int dtype, void* stream) {
   if (int rc = check_dtype(dtype)) return rc;
   if (T < 0 || T > kMaxDim || Hq <= 0 || Hkv <= 0 || max_pos <= 0 || max_pos > kMaxDim)
     return fail(TVQ_E_INVALID, "invalid T / heads / max_pos");
@@ -232,10 +233,17 @@ int tvq_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positio
   if (head_dim != 128) return fail(TVQ_E_UNSUPPORTED, "head_dim must be 128, got %d", head_dim);
   if (!qkv || !positions || !cos_t || !sin_t || !q_out || !k_out) return fail(TVQ_E_INVALID, "null pointer argument");
   if ((q_weight == nullptr) != (k_weight == nullptr)) return fail(TVQ_E_INVALID, "give both norm weights or neither");
-  if (row_stride < (int64_t)(Hq + Hkv) * head_dim) return fail(TVQ_E_INVALID, "row_stride shorter than q|k");
-  if (T * (Hq + Hkv) / 4 + 1 > kMaxDim) return fail(TVQ_E_UNSUPPORTED, "too many (token, head) pairs");
+  const bool store = k_cache != nullptr;
+  if (store != (v_cache != nullptr) || store != (slots != nullptr))
+    return fail(TVQ_E_INVALID, "give k_cache, v_cache and slots together or none");
+  if (store && (num_slots <= 0 || num_slots > kMaxDim || max_len <= 0 || max_len > kMaxDim))
+    return fail(TVQ_E_INVALID, "invalid num_slots / max_len");
+  if (row_stride < (int64_t)(Hq + (store ? 2 : 1) * Hkv) * head_dim)
+    return fail(TVQ_E_INVALID, "row_stride shorter than the heads read");
+  if (T * (Hq + 2 * Hkv) / 4 + 1 > kMaxDim) return fail(TVQ_E_UNSUPPORTED, "too many (token, head) pairs");
   hipError_t e = launch_qk_norm_rope(qkv, row_stride, positions, cos_t, sin_t, q_weight, k_weight, eps, T, Hq, Hkv,
-                                     (int)max_pos, q_out, k_out, dtype == TVQ_DTYPE_BF16, (hipStream_t)stream);
+                                     (int)max_pos, q_out, k_out, k_cache, v_cache, slots, (int)num_slots,
+                                     (int)max_len, dtype == TVQ_DTYPE_BF16, (hipStream_t)stream);
   if (e != hipSuccess) return fail(TVQ_E_HIP, "qk_norm_rope launch failed: %s", hipGetErrorString(e));
   return ok();
 }

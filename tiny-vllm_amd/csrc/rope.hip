@@ -18,6 +18,12 @@
 //   y1 = round(n1 * cos - n2 * sin),  y2 = round(n2 * cos + n1 * sin)   (fp32)
 // With no norm weights (models with q/k bias instead of q/k norm) only the
 // rotation is applied.
+//
+// Optionally (prefill) the kernel also stores each token's rotated key and its
+// value into the per-sequence KV cache [slots, Hkv, max_len, D] at (the
+// token's slot, its position), replacing the reference's store_kvcache
+// (attention.py:10-40) for the prompt tokens; v heads are then extra work
+// items that only copy.
 #include "tvq_common.h"
 #include "tvq_internal.h"
 
@@ -39,15 +45,35 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
                                                            const uint16_t* __restrict__ qw,
                                                            const uint16_t* __restrict__ kw, float eps, int T_, int Hq,
                                                            int Hkv, int max_pos, uint16_t* __restrict__ q_out,
-                                                           uint16_t* __restrict__ k_out) {
+                                                           uint16_t* __restrict__ k_out, uint16_t* __restrict__ k_cache,
+                                                           uint16_t* __restrict__ v_cache,
+                                                           const int64_t* __restrict__ slots, int num_slots,
+                                                           int max_len) {
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int heads = Hq + Hkv;
+  const bool store = k_cache != nullptr;
+  const int heads = Hq + Hkv + (store ? Hkv : 0);
   if (item >= (int64_t)T_ * heads) return;
   const int64_t t = item / heads;
   const int h = (int)(item % heads);
   const bool is_q = h < Hq;
   const uint16_t* src = qkv + t * row_stride + (int64_t)h * kD;
+  // cache destination of this token (only for the k and v heads of a store)
+  uint16_t* cache_row = nullptr;
+  if (store && !is_q) {
+    const int64_t slot = slots[t];
+    const int64_t pos = positions[t];
+    const int kvh = h < Hq + Hkv ? h - Hq : h - Hq - Hkv;
+    if (slot >= 0 && slot < num_slots && pos >= 0 && pos < max_len)
+      cache_row = (h < Hq + Hkv ? k_cache : v_cache) + ((slot * Hkv + kvh) * (int64_t)max_len + pos) * kD;
+  }
+  if (h >= Hq + Hkv) {  // value head: copy to the cache only
+    if (cache_row) {
+      cache_row[lane] = src[lane];
+      cache_row[lane + 64] = src[lane + 64];
+    }
+    return;
+  }
   float x1 = to_float<T>(src[lane]);
   float x2 = to_float<T>(src[lane + 64]);
   if constexpr (kNorm) {
@@ -64,27 +90,35 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
   const float y1 = x1 * c - x2 * s;
   const float y2 = x2 * c + x1 * s;
   uint16_t* dst = is_q ? q_out + (t * Hq + h) * kD : k_out + (t * Hkv + (h - Hq)) * kD;
-  dst[lane] = from_float<T>(y1);
-  dst[lane + 64] = from_float<T>(y2);
+  const uint16_t o1 = from_float<T>(y1), o2 = from_float<T>(y2);
+  dst[lane] = o1;
+  dst[lane + 64] = o2;
+  if (cache_row) {
+    cache_row[lane] = o1;
+    cache_row[lane + 64] = o2;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positions, const float* cos_t,
                                const float* sin_t, const void* q_weight, const void* k_weight, float eps, int64_t T_,
-                               int Hq, int Hkv, int max_pos, void* q_out, void* k_out, bool bf16,
-                               hipStream_t stream) {
-  const int64_t items = T_ * (Hq + Hkv);
+                               int Hq, int Hkv, int max_pos, void* q_out, void* k_out, void* k_cache, void* v_cache,
+                               const int64_t* slots, int num_slots, int max_len, bool bf16, hipStream_t stream) {
+  const int64_t items = T_ * (Hq + Hkv + (k_cache ? Hkv : 0));
   const dim3 grid((unsigned)((items + 3) / 4)), block(256);
   auto X = static_cast<const uint16_t*>(qkv);
   auto QW = static_cast<const uint16_t*>(q_weight);
   auto KW = static_cast<const uint16_t*>(k_weight);
   auto QO = static_cast<uint16_t*>(q_out);
   auto KO = static_cast<uint16_t*>(k_out);
+  auto KC = static_cast<uint16_t*>(k_cache);
+  auto VC = static_cast<uint16_t*>(v_cache);
   const bool norm = q_weight != nullptr;
 #define TVQ_ROPE(TT, NN)                                                                                       \
   qk_norm_rope_kernel<TT, NN><<<grid, block, 0, stream>>>(X, row_stride, positions, cos_t, sin_t, QW, KW, eps, \
-                                                          (int)T_, Hq, Hkv, max_pos, QO, KO)
+                                                          (int)T_, Hq, Hkv, max_pos, QO, KO, KC, VC, slots, num_slots, \
+                                                          max_len)
   if (bf16) {
     if (norm) TVQ_ROPE(BF16, true); else TVQ_ROPE(BF16, false);
   } else {

@@ -37,7 +37,8 @@ hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* 
                                    int num_slots, float scale, void* out, bool bf16, hipStream_t stream);
 hipError_t launch_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positions, const float* cos_t,
                                const float* sin_t, const void* q_weight, const void* k_weight, float eps, int64_t T_,
-                               int Hq, int Hkv, int max_pos, void* q_out, void* k_out, bool bf16, hipStream_t stream);
+                               int Hq, int Hkv, int max_pos, void* q_out, void* k_out, void* k_cache, void* v_cache,
+                               const int64_t* slots, int num_slots, int max_len, bool bf16, hipStream_t stream);
 hipError_t launch_prefill_attention(const void* q, const void* k, const void* v, int64_t v_stride,
                                     const int32_t* blocks, int nblocks, int Hq, int Hkv, float scale, void* out,
                                     bool bf16, hipStream_t stream);

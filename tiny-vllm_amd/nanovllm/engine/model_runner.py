@@ -182,8 +182,7 @@ class ModelRunner:
                 set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
                             slot_mapping=self._to_gpu([s.slot for s in seqs], torch.int64),
                             attn_blocks=blocks.pin_memory().cuda(non_blocking=True),
-                            token_slots=self._to_gpu([s.slot for s in seqs for _ in range(len(s))], torch.int64),
-                            token_pos=self._to_gpu(pos, torch.int64))
+                            token_slots=self._to_gpu([s.slot for s in seqs for _ in range(len(s))], torch.int64))
             else:
                 set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
                             slot_mapping=torch.tensor([s.slot for s in seqs]))

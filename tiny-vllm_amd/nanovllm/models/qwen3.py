@@ -79,12 +79,9 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = None  # set by the engine
 
     def _prefill_gpu(self, q, k, v, ctx) -> torch.Tensor:
-        """Store every prompt token's K/V at (its sequence's slot, its
-        position) in one batched copy, then run the HIP varlen causal
-        attention over the packed prompts."""
-        if self.k_cache is not None and ctx.token_slots is not None:
-            self.k_cache[ctx.token_slots, :, ctx.token_pos] = k
-            self.v_cache[ctx.token_slots, :, ctx.token_pos] = v
+        """HIP varlen causal attention over the packed prompts. The prompt
+        tokens' K/V were already stored into their cache slots by the fused
+        q/k-norm + rotary kernel (Qwen3Attention.forward)."""
         return _hip.prefill_attention(q, k, v, ctx.attn_blocks, self.scale)
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -169,8 +166,12 @@ class Qwen3Attention(nn.Module):
             qw = self.q_norm.weight if self.qk_norm else None
             kw = self.k_norm.weight if self.qk_norm else None
             eps = self.q_norm.eps if self.qk_norm else 0.0
+            ctx = get_context()
+            store = ctx.is_prefill and ctx.token_slots is not None and self.attn.k_cache is not None
             q, k = _hip.qk_norm_rope(qkv, positions, self.rotary_emb.cos, self.rotary_emb.sin, qw, kw, eps,
-                                     self.num_heads, self.num_kv_heads, self.head_dim)
+                                     self.num_heads, self.num_kv_heads, self.head_dim,
+                                     self.attn.k_cache if store else None, self.attn.v_cache if store else None,
+                                     ctx.token_slots if store else None)
             v = qkv[:, self.q_size + self.kv_size:].view(-1, self.num_kv_heads, self.head_dim)
         else:
             q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)

@@ -44,7 +44,7 @@ SYMBOLS = (
     ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_qk_norm_rope", _INT, (_VP, _I64, _VP, _VP, _VP, _VP, _VP, ctypes.c_float, _I64, _INT, _INT, _INT, _I64,
-                                _VP, _VP, _INT, _VP)),
+                                _VP, _VP, _VP, _VP, _VP, _I64, _I64, _INT, _VP)),
     ("tvq_prefill_attention", _INT, (_VP, _VP, _VP, _I64, _VP, _I64, _INT, _INT, _INT, ctypes.c_float, _VP, _INT,
                                      _VP)),
     ("tvq_decode_attention", _INT, (_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _INT, _INT, _INT, _I64,
@@ -338,10 +338,14 @@ def decode_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, 
 
 def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                  q_weight: torch.Tensor | None, k_weight: torch.Tensor | None, eps: float, num_heads: int,
-                 num_kv_heads: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+                 num_kv_heads: int, head_dim: int, k_cache: torch.Tensor | None = None,
+                 v_cache: torch.Tensor | None = None, slots: torch.Tensor | None = None
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
     """q/k of a packed qkv [T, >= (Hq+Hkv)*D] (row-contiguous): per-head
     RMSNorm (when weights are given) and rotate-half rotary embedding.
-    Returns q [T, Hq, D], k [T, Hkv, D]."""
+    Returns q [T, Hq, D], k [T, Hkv, D]. With caches [S, Hkv, L, D] and
+    per-token int64 slots, each token's key and value (the heads after the
+    keys in qkv) are also stored at (slot, position)."""
     lib = load_library()
     dev = qkv.device
     _require(qkv.is_cuda and qkv.dim() == 2 and qkv.stride(1) == 1, "qkv must be a row-contiguous 2-D GPU tensor")
@@ -359,10 +363,20 @@ def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, 
     k = torch.empty((t, num_kv_heads, head_dim), dtype=qkv.dtype, device=dev)
     if t == 0:
         return q, k
+    store = k_cache is not None
+    if store:
+        _require(v_cache is not None and slots is not None, "k_cache, v_cache and slots go together")
+        _require(k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape and
+                 k_cache.dim() == 4 and k_cache.shape[1] == num_kv_heads and k_cache.shape[3] == head_dim and
+                 k_cache.dtype == qkv.dtype, "caches must be contiguous [slots, Hkv, max_len, D] of qkv's dtype")
+        _require(slots.is_cuda and slots.dtype == torch.int64 and slots.is_contiguous() and slots.numel() == t,
+                 "slots must be contiguous int64 [T] on the GPU")
     with torch.cuda.device(dev):
         rc = lib.tvq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                   _ptr(q_weight), _ptr(k_weight), eps, t, num_heads, num_kv_heads, head_dim,
-                                  cos.shape[0], q.data_ptr(), k.data_ptr(), _TORCH_TO_TVQ[qkv.dtype], _stream(dev))
+                                  cos.shape[0], q.data_ptr(), k.data_ptr(), _ptr(k_cache), _ptr(v_cache),
+                                  _ptr(slots), k_cache.shape[0] if store else 0, k_cache.shape[2] if store else 0,
+                                  _TORCH_TO_TVQ[qkv.dtype], _stream(dev))
     _check(rc, "tvq_qk_norm_rope")
     return q, k
 

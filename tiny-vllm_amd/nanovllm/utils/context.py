@@ -21,10 +21,9 @@ class Context:
     kv_lo: int = 0   # decode: KV-cache slot range of the running batch
     kv_hi: int = 0
     # prefill on the GPU: the attention kernel's 64-query block table and,
-    # per packed token, its cache slot and position (for the KV-cache store)
+    # per packed token, its cache slot (for the KV-cache store)
     attn_blocks: torch.Tensor | None = None
     token_slots: torch.Tensor | None = None
-    token_pos: torch.Tensor | None = None
 
 
 _CONTEXT = Context()
@@ -35,11 +34,10 @@ def get_context() -> Context:
 
 
 def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0, slot_mapping=None,
-                context_lens=None, block_tables=None, kv_lo=0, kv_hi=0, attn_blocks=None, token_slots=None,
-                token_pos=None) -> None:
+                context_lens=None, block_tables=None, kv_lo=0, kv_hi=0, attn_blocks=None, token_slots=None) -> None:
     global _CONTEXT
     _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, slot_mapping,
-                       context_lens, block_tables, kv_lo, kv_hi, attn_blocks, token_slots, token_pos)
+                       context_lens, block_tables, kv_lo, kv_hi, attn_blocks, token_slots)
 
 
 def reset_context() -> None:
