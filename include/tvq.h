@@ -175,13 +175,21 @@ int tvq_decode_attention(const void* q, int64_t q_stride, const void* k_new,
  *   cos_t, sin_t [max_pos, head_dim/2] fp32
  *   q_weight, k_weight [head_dim] in `dtype`, or both NULL (rotation only)
  *   q_out [T, Hq, head_dim], k_out [T, Hkv, head_dim] contiguous
+ *   k_cache, v_cache [num_slots, Hkv, max_len, head_dim] and slots [T] int64,
+ *          or all NULL: when given, each token's rotated key and its value
+ *          (read from qkv after the keys) are also stored at
+ *          (slots[t], positions[t]) of the caches, replacing store_kvcache
+ *          (attention.py:10-40) for prompt tokens; tokens whose slot or
+ *          position is out of range are not stored.
  * head_dim must be 128. */
 int tvq_qk_norm_rope(const void* qkv, int64_t row_stride,
                      const int64_t* positions, const float* cos_t,
                      const float* sin_t, const void* q_weight,
                      const void* k_weight, float eps, int64_t T, int Hq,
                      int Hkv, int head_dim, int64_t max_pos, void* q_out,
-                     void* k_out, int dtype, void* stream);
+                     void* k_out, void* k_cache, void* v_cache,
+                     const int64_t* slots, int64_t num_slots, int64_t max_len,
+                     int dtype, void* stream);
 
 /* Causal attention over the packed prompts of a prefill step (no cached
  * prefix). Replaces flash_attn_varlen_func(q, k, v, cu_seqlens..., causal=True)

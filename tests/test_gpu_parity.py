@@ -68,6 +68,34 @@ def test_act_quant_ties_half_even(hiplib):
     np.testing.assert_array_equal(xq.cpu().numpy()[0], expect)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_act_quant_near_ties_bit_exact(hiplib, dtype):
+    """Rows built so that x/s lands on, or within a few ulps of, half-integers
+    for non-power-of-two scales: the kernels' multiply-by-1/s fast path must
+    hand exactly these to the IEEE divide (bit-exact vs the oracle), in
+    act-quant and in the fused producers' quantization."""
+    from nanovllm.quantization import _hip
+    rng = np.random.default_rng(5)
+    rows = []
+    for _ in range(512):
+        amax = np.float32(rng.uniform(0.5, 40.0))
+        s = max(np.float32(amax / np.float32(127.0)), np.float32(1e-8))
+        k = rng.integers(-126, 126, 255).astype(np.float32)
+        t = (k + np.float32(0.5)) * s * (1 + rng.integers(-4, 5, 255) * np.float32(2.0 ** -23))
+        rows.append(np.concatenate([[amax], t]).astype(np.float32))
+    x = torch.from_numpy(np.stack(rows)).to(dtype)   # rounding to 16 bits keeps many exact/near ties
+    q_ref, s_ref = oracle.c_act_quant(bits16(x), is_bf16=dtype == torch.bfloat16)
+    xq, sc = _hip.act_quant(x.to(_dev()))
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(xq.cpu().numpy(), q_ref)
+    # fused SiLU-and-mul quantization on rows whose SiLU output is x (u = x / silu(g) is awkward;
+    # use the RMSNorm producer with unit weight on rows of constant RMS instead: its y is x * r)
+    y, q = _hip.rmsnorm(x.to(_dev()), torch.ones(256, dtype=dtype, device=_dev()), 1e-6, out=True, quant=True)
+    rq, rs = oracle.c_act_quant(bits16(y.cpu()), is_bf16=dtype == torch.bfloat16)
+    np.testing.assert_array_equal(q[0].cpu().numpy(), rq)
+    np.testing.assert_array_equal(q[1].cpu().numpy().view(np.uint32), rs.view(np.uint32))
+
+
 # ---------------------------------------------------------------- W8A8
 
 # (M, N, K) covering skinny (M <= 64), tiled, ragged edges and the generic path.

@@ -5,7 +5,9 @@
 // elementwise/reduction launches with fp32 temporaries:
 //   amax   = max_k |float(x[m,k])|                (exact, order-free)
 //   s      = max(amax / 127.0f, eps)               (IEEE RN divide)
-//   xq     = clamp(rint(float(x) / s), -127, 127)  (IEEE RN divide, ties-to-even)
+//   xq     = clamp(rint(float(x) / s), -127, 127)  (IEEE RN divide, ties-to-even;
+//            computed as a multiply by RN(1/s) with an exact-divide fallback
+//            near half-integers, see quant_code)
 //
 // One wave (64 lanes) owns one row; a 256-thread workgroup handles 4 rows.
 // HBM traffic is the algorithmic minimum for rows that fit the register
@@ -37,20 +39,17 @@ __device__ __forceinline__ float absmax8(u32x4 v) {
   return m;
 }
 
-__device__ __forceinline__ uint32_t q1(float x, float s) {
-  // __fdiv_rn is the IEEE-754 correctly rounded single-precision divide.
-  float t = rintf(__fdiv_rn(x, s));
-  t = fminf(fmaxf(t, -127.0f), 127.0f);
-  return (uint32_t)((int32_t)t & 0xff);
+__device__ __forceinline__ uint32_t q1(float x, float s, float rs) {
+  return (uint32_t)((int32_t)quant_code(x, s, rs) & 0xff);
 }
 
 template <typename T>
-__device__ __forceinline__ u32x2 quant8(u32x4 v, float s) {
+__device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs) {
   u32x2 r;
-  r.x = q1(to_float<T>((uint16_t)(v[0] & 0xffffu)), s) | (q1(to_float<T>((uint16_t)(v[0] >> 16)), s) << 8) |
-        (q1(to_float<T>((uint16_t)(v[1] & 0xffffu)), s) << 16) | (q1(to_float<T>((uint16_t)(v[1] >> 16)), s) << 24);
-  r.y = q1(to_float<T>((uint16_t)(v[2] & 0xffffu)), s) | (q1(to_float<T>((uint16_t)(v[2] >> 16)), s) << 8) |
-        (q1(to_float<T>((uint16_t)(v[3] & 0xffffu)), s) << 16) | (q1(to_float<T>((uint16_t)(v[3] >> 16)), s) << 24);
+  r.x = q1(to_float<T>((uint16_t)(v[0] & 0xffffu)), s, rs) | (q1(to_float<T>((uint16_t)(v[0] >> 16)), s, rs) << 8) |
+        (q1(to_float<T>((uint16_t)(v[1] & 0xffffu)), s, rs) << 16) | (q1(to_float<T>((uint16_t)(v[1] >> 16)), s, rs) << 24);
+  r.y = q1(to_float<T>((uint16_t)(v[2] & 0xffffu)), s, rs) | (q1(to_float<T>((uint16_t)(v[2] >> 16)), s, rs) << 8) |
+        (q1(to_float<T>((uint16_t)(v[3] & 0xffffu)), s, rs) << 16) | (q1(to_float<T>((uint16_t)(v[3] >> 16)), s, rs) << 24);
   return r;
 }
 
@@ -82,14 +81,15 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
   amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);
   if (lane == 0) a_scales[row] = s;
+  const float rs = __fdiv_rn(1.0f, s);
 
 #pragma unroll
   for (int it = 0; it < kCacheIters; ++it) {
     const int64_t v = (int64_t)it * kWave + lane;
-    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = quant8<T>(cache[it], s);
+    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = quant8<T>(cache[it], s, rs);
   }
   for (int64_t v = (int64_t)kCacheIters * kWave + lane; v < nvec; v += kWave) {
-    *reinterpret_cast<u32x2*>(qr + v * 8) = quant8<T>(ldg128(xr + v * 8), s);
+    *reinterpret_cast<u32x2*>(qr + v * 8) = quant8<T>(ldg128(xr + v * 8), s, rs);
   }
 }
 
@@ -107,7 +107,8 @@ __global__ __launch_bounds__(256) void act_quant_scalar_kernel(const uint16_t* _
   amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);
   if (lane == 0) a_scales[row] = s;
-  for (int64_t k = lane; k < K; k += kWave) xq[row * K + k] = (int8_t)q1(to_float<T>(xr[k]), s);
+  const float rs = __fdiv_rn(1.0f, s);
+  for (int64_t k = lane; k < K; k += kWave) xq[row * K + k] = (int8_t)q1(to_float<T>(xr[k]), s, rs);
 }
 
 }  // namespace

@@ -43,10 +43,7 @@ __device__ __forceinline__ float wmax(float v) {
   return v;
 }
 
-__device__ __forceinline__ int8_t qcode(float y, float s) {
-  float t = rintf(__fdiv_rn(y, s));
-  return (int8_t)(int)fminf(fmaxf(t, -127.0f), 127.0f);
-}
+__device__ __forceinline__ int8_t qcode(float y, float s, float rs) { return (int8_t)(int)quant_code(y, s, rs); }
 
 template <typename T>
 __device__ __forceinline__ float elt(const u32x4& v, int i) {
@@ -75,6 +72,7 @@ __device__ __forceinline__ void quant_store(const u32x4 (&y)[kIters], int nvec, 
   amax = wmax(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);
   if (lane == 0) *srow = s;
+  const float rs = __fdiv_rn(1.0f, s);
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     const int v = it * kWave + lane;
@@ -82,8 +80,8 @@ __device__ __forceinline__ void quant_store(const u32x4 (&y)[kIters], int nvec, 
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        lo |= (uint32_t)(uint8_t)qcode(elt<T>(y[it], i), s) << (8 * i);
-        hi |= (uint32_t)(uint8_t)qcode(elt<T>(y[it], i + 4), s) << (8 * i);
+        lo |= (uint32_t)(uint8_t)qcode(elt<T>(y[it], i), s, rs) << (8 * i);
+        hi |= (uint32_t)(uint8_t)qcode(elt<T>(y[it], i + 4), s, rs) << (8 * i);
       }
       *reinterpret_cast<u32x2*>(qr + (int64_t)v * 8) = u32x2{lo, hi};
     }
@@ -218,9 +216,10 @@ __global__ __launch_bounds__(256) void rmsnorm_scalar_kernel(const uint16_t* __r
   amax = wmax(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f);
   if (lane == 0) a_scales[row] = s;
+  const float rs = __fdiv_rn(1.0f, s);
   for (int k = lane; k < K; k += kWave) {
     float h;
-    xq[row * K + k] = qcode(rms_y<T>(xr, rr, w, k, r, &h), s);
+    xq[row * K + k] = qcode(rms_y<T>(xr, rr, w, k, r, &h), s, rs);
     if (rr) rr[k] = from_float<T>(h);
   }
 }
@@ -247,7 +246,8 @@ __global__ __launch_bounds__(256) void silu_mul_scalar_kernel(const uint16_t* __
   amax = wmax(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f);
   if (lane == 0) a_scales[row] = s;
-  for (int k = lane; k < I; k += kWave) xq[row * I + k] = qcode(val(k), s);
+  const float rs = __fdiv_rn(1.0f, s);
+  for (int k = lane; k < I; k += kWave) xq[row * I + k] = qcode(val(k), s, rs);
 }
 
 }  // namespace

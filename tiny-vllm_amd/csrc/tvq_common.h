@@ -139,4 +139,18 @@ __device__ __forceinline__ float epi_w8a8(int32_t acc, float as, float ws, float
   return __builtin_fmaf((float)acc * as, ws, b);
 }
 
+// Per-token int8 code of x for scale s, bit-identical to
+// clamp(rint(x / s), -127, 127) with an IEEE round-to-nearest divide
+// (quantize_int8_per_row_dynamic, reference utils.py:28-32), given
+// rs = RN(1/s). The multiply d = RN(x * rs) is within 2^-16 of RN(x / s)
+// for |x / s| <= 128 (two roundings of relative size <= 2^-24 each), and rint
+// changes only at half-integers; so unless d lies within 2^-14 of one, rint(d)
+// equals rint(RN(x / s)). Those rare ties and near-ties take the exact divide.
+__device__ __forceinline__ float quant_code(float x, float s, float rs) {
+  const float d = x * rs;
+  float t = rintf(d);
+  if (fabsf(fabsf(d - truncf(d)) - 0.5f) < 0x1p-14f) t = rintf(__fdiv_rn(x, s));
+  return fminf(fmaxf(t, -127.0f), 127.0f);
+}
+
 }  // namespace tvq
