@@ -19,11 +19,14 @@
 // Any consistent assignment of k to (lane group, register slot) yields the
 // same dot products, so A and B only have to agree with each other.
 //
-// A workgroup of W waves (W = 4, 8 or 16, chosen so that each wave needs about
-// one run over K) owns 16*RG output channels; its waves split K in interleaved
-// runs of U 64-wide chunks and are reduced through LDS at the end in a fixed
-// order (deterministic output). More waves per row group means more weight
-// loads in flight per workgroup and shorter latency chains per wave.
+// A workgroup of W waves owns 16*RG output channels; its waves split K into
+// contiguous ranges of U-chunk runs (64 k per chunk) and are reduced through
+// LDS at the end in a fixed order (deterministic output). W = 4 when there are
+// enough workgroups to fill the chip (N >= 16384); otherwise 8 or 16 so that
+// each wave needs about one run over K, which keeps more weight loads in
+// flight per workgroup and the latency chains short.
+#include <type_traits>
+
 #include "tvq_common.h"
 #include "tvq_internal.h"
 
@@ -47,7 +50,7 @@ __global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restr
   constexpr int kXRegs = kW8A8 ? 1 : 2;  // 16-byte x vectors per (chunk, m-group)
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -59,41 +62,45 @@ __global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restr
 #pragma unroll
     for (int j = 0; j < MG; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 
-  // Per-lane row pointers (clamped rows are never dereferenced).
+  // Per-lane row pointers. Rows past N (weights) or M (tokens) are clamped to
+  // the last row: they are read but only feed accumulator entries whose
+  // outputs are never stored, so the loads need no predicate.
   const int8_t* wrow[RG];
-  bool wok[RG];
 #pragma unroll
   for (int i = 0; i < RG; ++i) {
     const int n = n0 + 16 * i + r;
-    wok[i] = n < N;
-    wrow[i] = qw + (int64_t)(wok[i] ? n : 0) * K + 16 * g;
+    wrow[i] = qw + (int64_t)(n < N ? n : N - 1) * K + 16 * g;
   }
   const char* xrow[MG];
-  bool xok[MG];
 #pragma unroll
   for (int j = 0; j < MG; ++j) {
     const int m = 16 * j + r;
-    xok[j] = m < M;
-    xrow[j] = static_cast<const char*>(xv) + (int64_t)(xok[j] ? m : 0) * K * (kW8A8 ? 1 : 2) + 16 * g * (kW8A8 ? 1 : 2);
+    xrow[j] = static_cast<const char*>(xv) + ((int64_t)(m < M ? m : M - 1) * K + 16 * g) * (kW8A8 ? 1 : 2);
   }
 
+  // Each wave owns one contiguous range of whole U-chunk runs, so its reads
+  // of every weight row are contiguous.
   const int nchunks = (K + 63) >> 6;
-  for (int c0 = wave * U; c0 < nchunks; c0 += kWaves * U) {
+  const int cpw = ((nchunks + kWaves * U - 1) / (kWaves * U)) * U;
+  const int cend = min(nchunks, (wave + 1) * cpw);
+
+  // One run of U chunks: loads (unpredicated when kGuard is false), then MFMAs.
+  auto run = [&](int c0, auto guard) {
+    constexpr bool kGuard = decltype(guard)::value;
     u32x4 wv[U][RG];
     u32x4 xvv[U][MG][kXRegs];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kb = (c0 + u) * 64 + 16 * g;  // first k of this lane's 16-k slice
-      const bool kok = kb < K;
+      // kGuard: chunk inside this wave's range and the lane's 16 k inside K.
+      const bool kok = !kGuard || ((c0 + u) < cend && (c0 + u) * 64 + 16 * g < K);
 #pragma unroll
-      for (int i = 0; i < RG; ++i)
-        wv[u][i] = (kok && wok[i]) ? ldg128_stream(wrow[i] + (int64_t)(c0 + u) * 64) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < RG; ++i) wv[u][i] = kok ? ldg128_stream(wrow[i] + (int64_t)(c0 + u) * 64) : u32x4{0, 0, 0, 0};
 #pragma unroll
       for (int j = 0; j < MG; ++j) {
 #pragma unroll
         for (int h = 0; h < kXRegs; ++h) {
           const int64_t off = (int64_t)(c0 + u) * 64 * (kW8A8 ? 1 : 2) + 16 * h;
-          xvv[u][j][h] = (kok && xok[j]) ? ldg128(xrow[j] + off) : u32x4{0, 0, 0, 0};
+          xvv[u][j][h] = kok ? ldg128(xrow[j] + off) : u32x4{0, 0, 0, 0};
         }
       }
     }
@@ -119,6 +126,13 @@ __global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restr
         }
       }
     }
+  };
+  for (int c0 = wave * cpw; c0 < cend; c0 += U) {
+    // The run is fully valid unless it reaches past the wave's range or K.
+    if (c0 + U <= cend && (c0 + U) * 64 <= K)
+      run(c0, std::false_type{});
+    else
+      run(c0, std::true_type{});
   }
 
   // Cross-wave reduction in a fixed order (wave 0 + 1 + 2 + 3).
@@ -193,6 +207,7 @@ hipError_t launch_rg(const GemmArgs& a, hipStream_t stream) {
   if constexpr (RG * MG <= 2) {
     if (runs > 8) return launch_w<T, kW8A8, kRaw, MG, RG, 16>(a, stream);
   }
+  if (a.N >= 16384) return launch_w<T, kW8A8, kRaw, MG, RG, 4>(a, stream);
   if constexpr (RG * MG <= 4) {
     if (runs > 4) return launch_w<T, kW8A8, kRaw, MG, RG, 8>(a, stream);
   }
