@@ -134,6 +134,9 @@ class Launcher:
     def __init__(self, lib, dev):
         self.lib = lib
         self.dev = dev
+        from nanovllm.quantization import _hip
+        ws = _hip.gemm_workspace(dev)   # split-K workspace, as the Python layer passes it
+        self.ws = (ws.data_ptr(), ws.numel())
 
     def stream(self):
         return torch.cuda.current_stream(self.dev).cuda_stream
@@ -147,20 +150,20 @@ class Launcher:
         m, k = xq.shape
         n = q.shape[0]
         return lambda: self._ck(self.lib.tvq_w8a8_gemm(xq.data_ptr(), a_s.data_ptr(), q.data_ptr(), s.data_ptr(),
-                                                       None, y.data_ptr(), 1, m, n, k, self.stream()))
+                                                       None, y.data_ptr(), 1, m, n, k, *self.ws, self.stream()))
 
     def w8a8_linear(self, x, q, s, y, xq, a_s):
         m, k = x.shape
         n = q.shape[0]
         return lambda: self._ck(self.lib.tvq_w8a8_linear(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None,
                                                          y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(),
-                                                         self.stream()))
+                                                         *self.ws, self.stream()))
 
     def w8a16(self, x, q, s, y):
         m, k = x.shape
         n = q.shape[0]
         return lambda: self._ck(self.lib.tvq_w8a16_gemm(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None,
-                                                        y.data_ptr(), m, n, k, self.stream()))
+                                                        y.data_ptr(), m, n, k, *self.ws, self.stream()))
 
     def _ck(self, rc):
         if rc != 0:

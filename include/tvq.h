@@ -20,6 +20,16 @@
  *   bias     [N]     same dtype as the output, or NULL
  *   y        [M, N]  bf16 or fp16 output (int32 for tvq_w8a8_gemm_i32)
  *
+ * GEMM workspace: the GEMM entry points take an optional device workspace
+ * (workspace, workspace_bytes; NULL/0 disables its use). With one, decode-
+ * size calls whose output tiles do not fill the GPU split K over several
+ * workgroups and reduce the partial sums inside the same launch, in a fixed
+ * order (results do not depend on scheduling). The workspace must be
+ * 256-byte aligned and zero-filled once when it is allocated; every call
+ * leaves it ready for the next. Calls that share a workspace must be ordered
+ * (one stream). tvq_gemm_workspace_bytes() gives the size that enables every
+ * split; a smaller one only limits them.
+ *
  * Return codes: TVQ_OK (0) on success, a negative TVQ_E* code otherwise;
  * tvq_last_error() then describes the failure (thread-local string).
  */
@@ -32,7 +42,7 @@
 extern "C" {
 #endif
 
-#define TVQ_ABI_VERSION 2
+#define TVQ_ABI_VERSION 3
 
 /* Activation / output element types. */
 enum tvq_dtype {
@@ -87,7 +97,8 @@ int tvq_act_quant(const void* x, int dtype, int64_t M, int64_t K, float eps,
  * (nanovllm/quantization/cuda.py:261-274). */
 int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight,
                    const float* scales, const void* bias, void* y, int64_t M,
-                   int64_t N, int64_t K, void* stream);
+                   int64_t N, int64_t K, void* workspace,
+                   int64_t workspace_bytes, void* stream);
 
 /* W8A8: acc[m,n] = sum_k xq[m,k]·qweight[n,k] (exact int32),
  *   y[m,n] = out((float(acc)·a_scales[m])·w_scales[n] + bias[n]).
@@ -98,7 +109,8 @@ int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight,
 int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales,
                   const int8_t* qweight, const float* w_scales,
                   const void* bias, void* y, int out_dtype, int64_t M,
-                  int64_t N, int64_t K, void* stream);
+                  int64_t N, int64_t K, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 
 /* The raw exact int32 accumulator acc[m,n] = sum_k xq[m,k]·qweight[n,k] of
  * the W8A8 path, written to y_i32 [M, N], using the same kernel selection as
@@ -106,7 +118,8 @@ int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales,
  * accumulator the reference forms inside w8a8_gemm_wmma_kernel
  * (w8a8_gemm.cu:336-375) so it can be checked bit-exactly. */
 int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32,
-                      int64_t M, int64_t N, int64_t K, void* stream);
+                      int64_t M, int64_t N, int64_t K, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 /* Fused W8A8 linear: tvq_act_quant(x) into the caller's xq / a_scales buffers
  * followed by tvq_w8a8_gemm, both on `stream`. Replaces the pair
@@ -115,7 +128,13 @@ int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32,
 int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight,
                     const float* w_scales, const void* bias, void* y,
                     int64_t M, int64_t N, int64_t K, int8_t* xq_buf,
-                    float* a_scales_buf, void* stream);
+                    float* a_scales_buf, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* Size in bytes of a GEMM workspace that enables every split-K launch (see
+ * the top of this file). No reference counterpart: the reference's kernels
+ * never split K. */
+int64_t tvq_gemm_workspace_bytes(void);
 
 /* Fused RMSNorm producer of a projection input. Replaces RMSNorm.rms_forward
  * / add_rms_forward (nanovllm/layers/layernorm.py:16-40), optionally followed

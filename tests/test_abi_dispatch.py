@@ -31,7 +31,8 @@ def _declared_symbols() -> list[str]:
 def test_header_declares_expected_entry_points():
     syms = _declared_symbols()
     for name in ("tvq_abi_version", "tvq_last_error", "tvq_select_path", "tvq_act_quant", "tvq_w8a16_gemm",
-                 "tvq_w8a8_gemm", "tvq_w8a8_gemm_i32", "tvq_w8a8_linear", "tvq_rmsnorm", "tvq_silu_mul"):
+                 "tvq_w8a8_gemm", "tvq_w8a8_gemm_i32", "tvq_w8a8_linear", "tvq_rmsnorm", "tvq_silu_mul",
+                 "tvq_gemm_workspace_bytes"):
         assert name in syms
 
 
@@ -44,14 +45,17 @@ def test_library_exports_every_declared_symbol(hiplib):
 
 
 def test_abi_version_and_errors_without_gpu(hiplib):
-    assert hiplib.tvq_abi_version() == 2
-    assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None) == -1
+    assert hiplib.tvq_abi_version() == 3
+    assert hiplib.tvq_gemm_workspace_bytes() >= 16 << 20
+    assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None, 0, None) == -1
     assert b"dtype" in hiplib.tvq_last_error()
-    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 1, 1, 16, None) == -1
+    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 1, 1, 16, None, 0, None) == -1
     assert b"null pointer" in hiplib.tvq_last_error()
-    assert hiplib.tvq_w8a8_gemm(None, None, None, None, None, None, 1, 1, 0, 16, None) == -1
+    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 1, 1, 16, 0x1010, 1 << 20, None) == -1
+    assert b"256-byte aligned" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a8_gemm(None, None, None, None, None, None, 1, 1, 0, 16, None, 0, None) == -1
     assert b"invalid shape" in hiplib.tvq_last_error()
-    assert hiplib.tvq_w8a8_gemm_i32(None, None, None, 1, 1, 1 << 40, None) == -2
+    assert hiplib.tvq_w8a8_gemm_i32(None, None, None, 1, 1, 1 << 40, None, 0, None) == -2
     assert b"2^31" in hiplib.tvq_last_error()
     assert hiplib.tvq_act_quant(None, 1, 4, 16, -1.0, None, None, None) == -1
     assert hiplib.tvq_rmsnorm(None, None, None, 1e-6, None, None, None, 1, 4, 16, None) == -1
@@ -62,7 +66,7 @@ def test_abi_version_and_errors_without_gpu(hiplib):
     assert b"without a_scales" in hiplib.tvq_last_error()
     assert hiplib.tvq_silu_mul(1, 1, None, None, 1, 0, 16, None) == 0
     # M == 0 is a valid no-op that launches nothing
-    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 0, 8, 16, None) == 0
+    assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 0, 8, 16, None, 0, None) == 0
     assert hiplib.tvq_last_error() == b""
 
 
@@ -74,6 +78,11 @@ def test_select_path_buckets(hiplib):
     assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "skinny_mfma_f16x_m16"
     assert sp(_hip.OP_W8A16, 16, 4096, 1024) == "skinny_mfma_f16x_m16"
     assert sp(_hip.OP_W8A16, 64, 4096, 1024) == "dma_mfma_f16x_32x64"     # 16 < M <= 64: DMA tiles
+    # split-K shapes (M <= 64, N < 16384, K >= 2048) take 64x64 tiles above M = 32; without a
+    # device the name carries no "_splitk" (the split count depends on the CU count)
+    assert sp(_hip.OP_W8A16, 64, 4096, 12288) == "dma_mfma_f16x_64x64"
+    assert sp(_hip.OP_W8A8, 48, 4096, 4096) == "dma_mfma_i8_64x64"
+    assert sp(_hip.OP_W8A16, 32, 4096, 4096) == "dma_mfma_f16x_32x64"
     assert sp(_hip.OP_W8A8, 17, 6144, 1024) == "dma_mfma_i8_32x64"
     assert sp(_hip.OP_W8A8, 64, 24576, 4096) == "dma_mfma_i8_64x128"     # wide N
     assert sp(_hip.OP_W8A16, 64, 24576, 4096) == "dma_mfma_f16x_64x128"

@@ -322,3 +322,107 @@ def test_hip_graph_capture_replay(hiplib):
         torch.cuda.synchronize()
         assert torch.equal(y16.view(torch.int16), ref16.view(torch.int16)), f"replay {i}"
         assert torch.equal(y8.view(torch.int16), ref8.view(torch.int16)), f"replay {i}"
+
+
+# ---------------------------------------------------------------- split-K
+
+# Decode-size shapes whose output tiles do not fill the GPU: K is split over
+# several workgroups and reduced in-kernel through the GEMM workspace.
+SPLIT_SHAPES = [(17, 1000, 2048), (24, 4096, 4096), (40, 6144, 4096), (64, 4096, 12288), (64, 1024, 3072),
+                (33, 136, 2048)]
+
+
+def _same_up_to_order(a, b, x, q, s):
+    """W8A16 outputs that differ only in the fp32 summation order: within one
+    bf16 rounding flip plus the fp32 reassociation bound K*2^-23*sum|terms|
+    (checked on a sample of rows)."""
+    rows = np.unique(np.linspace(0, x.shape[0] - 1, 6).astype(np.int64))
+    fa, fb = f32(a)[rows].astype(np.float64), f32(b)[rows].astype(np.float64)
+    mag = (np.abs(f32(x)[rows]).astype(np.float64) @ np.abs(q).astype(np.float64).T) * np.asarray(s)[None, :]
+    bound = np.abs(fb) * 2.0 ** -7 + mag * (x.shape[1] * 2.0 ** -23) + 1e-30
+    assert np.all(np.abs(fa - fb) <= bound), f"max excess {np.max(np.abs(fa - fb) - bound)}"
+
+
+@pytest.mark.parametrize("shape", SPLIT_SHAPES)
+def test_split_k_matches_unsplit(hiplib, shape):
+    """Split-K gives the unsplit kernel's exact int32 accumulators and W8A8
+    outputs, and W8A16 outputs equal up to fp32 summation order."""
+    from nanovllm.quantization import _hip
+    m, n, k = shape
+    for op in (_hip.OP_W8A8, _hip.OP_W8A16):
+        path = _hip.select_path(op, m, n, k)
+        _log_case(test="split_k", m=m, n=n, k=k, path=path)
+        assert path.endswith("_splitk"), path
+    d = _dev()
+    xq, a_s, q, w_s = _w8a8_inputs(m, n, k, seed=m * 5 + n + k)
+    xq_d, a_d, q_d, w_d = (torch.from_numpy(t).to(d) for t in (xq, a_s, q, w_s))
+    acc_s = _hip.w8a8_gemm_i32(xq_d, q_d)
+    acc_u = _hip.w8a8_gemm_i32(xq_d, q_d, split_k=False)
+    assert torch.equal(acc_s, acc_u)
+    rows = np.unique(np.linspace(0, m - 1, 8).astype(np.int64))
+    np.testing.assert_array_equal(acc_s.cpu().numpy()[rows], oracle.c_gemm_i32(xq[rows], q))
+    y_s = _hip.w8a8_gemm(xq_d, a_d, q_d, w_d, None, torch.bfloat16)
+    y_u = _hip.w8a8_gemm(xq_d, a_d, q_d, w_d, None, torch.bfloat16, split_k=False)
+    assert torch.equal(y_s.view(torch.int16), y_u.view(torch.int16))
+    x = make_activations(m, k, seed=m + 3 * n, outlier_frac=0.0).to(d)
+    h_s = _hip.w8a16_gemm(x, q_d, w_d)
+    h_u = _hip.w8a16_gemm(x, q_d, w_d, split_k=False)
+    _same_up_to_order(h_s, h_u, x, q, w_s)
+    _w8a16_check(h_s.cpu()[torch.from_numpy(rows)], x.cpu()[torch.from_numpy(rows)], torch.from_numpy(q),
+                 torch.from_numpy(w_s))
+
+
+def test_split_k_deterministic_and_workspace_reuse(hiplib):
+    """Repeated split calls give identical bits whatever order their work units
+    finish in, and a call leaves the workspace counters ready for the next
+    call of another shape."""
+    from nanovllm.quantization import _hip
+    d = _dev()
+    qa, sa = (t.to(d) for t in make_weights(4096, 4096, seed=21))
+    qb, sb = (t.to(d) for t in make_weights(1000, 3072, seed=22))
+    xa = make_activations(64, 4096, seed=23, outlier_frac=0.0).to(d)
+    xb = make_activations(40, 3072, seed=24, outlier_frac=0.0).to(d)
+    first_a = _hip.w8a16_gemm(xa, qa, sa)
+    first_b8 = _hip.w8a8_linear(xb, qb, sb)
+    for i in range(6):
+        ya = _hip.w8a16_gemm(xa, qa, sa)
+        yb8 = _hip.w8a8_linear(xb, qb, sb)
+        yb = _hip.w8a16_gemm(xb, qb, sb)
+        assert torch.equal(ya.view(torch.int16), first_a.view(torch.int16)), f"iteration {i}"
+        assert torch.equal(yb8.view(torch.int16), first_b8.view(torch.int16)), f"iteration {i}"
+        _same_up_to_order(yb, _hip.w8a16_gemm(xb, qb, sb, split_k=False), xb, qb.cpu().numpy(), sb.cpu().numpy())
+    ws = _hip.gemm_workspace(d)
+    torch.cuda.synchronize()
+    assert int(ws[: 64 * 1024].view(torch.int32).abs().sum()) == 0   # every tile counter back at zero
+
+
+def test_split_k_graph_replay(hiplib):
+    """Split-K launches captured in a HIP graph replay correctly every time."""
+    from nanovllm.quantization import _hip
+    d = _dev()
+    q, s = (t.to(d) for t in make_weights(4096, 4096, seed=31))
+    x = make_activations(48, 4096, seed=32).to(d)
+    assert _hip.select_path(_hip.OP_W8A16, 48, 4096, 4096).endswith("_splitk")
+    ref16 = _hip.w8a16_gemm(x, q, s)
+    ref8 = _hip.w8a8_linear(x, q, s)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        _hip.w8a16_gemm(x, q, s)
+        _hip.w8a8_linear(x, q, s)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y16 = _hip.w8a16_gemm(x, q, s)
+        y8 = _hip.w8a8_linear(x, q, s)
+    for i in range(4):
+        y16.zero_()
+        y8.zero_()
+        other = _hip.w8a16_gemm(x[:20], q, s)   # eager split call between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y16.view(torch.int16), ref16.view(torch.int16)), f"replay {i}"
+        assert torch.equal(y8.view(torch.int16), ref8.view(torch.int16)), f"replay {i}"
+        assert torch.equal(other.view(torch.int16), _hip.w8a16_gemm(x[:20], q, s).view(torch.int16))

@@ -51,6 +51,17 @@ int check_dtype(int dtype) {
 
 bool shape_vec_ok(int64_t K) { return K % 16 == 0; }
 
+// Recommended split-K workspace: the counter block plus the largest set of
+// partial tiles the split policy produces on a 256-CU device.
+constexpr int64_t kGemmWorkspaceBytes = (16 << 20) + (64 << 10);
+
+int check_workspace(const void* ws, int64_t bytes) {
+  if (ws == nullptr) return TVQ_OK;
+  if (((uintptr_t)ws & 255u) != 0) return fail(TVQ_E_INVALID, "workspace must be 256-byte aligned");
+  if (bytes < 0) return fail(TVQ_E_INVALID, "negative workspace size %lld", (long long)bytes);
+  return TVQ_OK;
+}
+
 int run_gemm(const GemmArgs& a, void* stream) {
   if (a.M == 0) return ok();
   hipError_t e;
@@ -79,7 +90,7 @@ Path select_gemm_path(const GemmArgs& a) {
 
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
-  if (M > kDmaMinM && dma_shape_ok(K)) return dma_path_name(w8a8, M, N);
+  if (M > kDmaMinM && dma_shape_ok(K)) return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
   if (M <= kSkinnyMaxM && stream_shape_ok(M, N, K)) {
     static const char* s8[4] = {"stream_mfma_i8_m16", "stream_mfma_i8_m32", "stream_mfma_i8_m48", "stream_mfma_i8_m64"};
     static const char* s16[4] = {"stream_mfma_f16x_m16", "stream_mfma_f16x_m32", "stream_mfma_f16x_m48",
@@ -95,7 +106,7 @@ const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool alig
     const int mg = M <= 0 ? 0 : (int)((M + 15) / 16) - 1;
     return w8a8 ? names8[mg] : names16[mg];
   }
-  if (dma_shape_ok(K)) return dma_path_name(w8a8, M, N);
+  if (dma_shape_ok(K)) return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
   return w8a8 ? "tiled_mfma_i8_128x128x128" : "tiled_mfma_f16x_128x128x64";
 }
 
@@ -131,44 +142,55 @@ int tvq_act_quant(const void* x, int dtype, int64_t M, int64_t K, float eps, int
   return ok();
 }
 
+int64_t tvq_gemm_workspace_bytes(void) { return kGemmWorkspaceBytes; }
+
 int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight, const float* scales, const void* bias, void* y,
-                   int64_t M, int64_t N, int64_t K, void* stream) {
+                   int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = check_dtype(dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
+  if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
   if (M == 0) return ok();
   if (!x || !qweight || !scales || !y) return fail(TVQ_E_INVALID, "null pointer argument");
-  GemmArgs a{x, nullptr, qweight, scales, bias, y, M, N, K, false, dtype == TVQ_DTYPE_BF16, false};
+  GemmArgs a{x, nullptr, qweight, scales, bias, y, M, N, K, false, dtype == TVQ_DTYPE_BF16, false, workspace,
+             workspace_bytes};
   return run_gemm(a, stream);
 }
 
 int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales, const int8_t* qweight, const float* w_scales,
-                  const void* bias, void* y, int out_dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+                  const void* bias, void* y, int out_dtype, int64_t M, int64_t N, int64_t K, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
   if (int rc = check_dtype(out_dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
+  if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
   if (M == 0) return ok();
   if (!xq || !a_scales || !qweight || !w_scales || !y) return fail(TVQ_E_INVALID, "null pointer argument");
-  GemmArgs a{xq, a_scales, qweight, w_scales, bias, y, M, N, K, true, out_dtype == TVQ_DTYPE_BF16, false};
+  GemmArgs a{xq, a_scales, qweight, w_scales, bias, y, M, N, K, true, out_dtype == TVQ_DTYPE_BF16, false, workspace,
+             workspace_bytes};
   return run_gemm(a, stream);
 }
 
 int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32, int64_t M, int64_t N, int64_t K,
-                      void* stream) {
+                      void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = check_dims(M, N, K)) return rc;
+  if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
   if (M == 0) return ok();
   if (!xq || !qweight || !y_i32) return fail(TVQ_E_INVALID, "null pointer argument");
-  GemmArgs a{xq, nullptr, qweight, nullptr, nullptr, y_i32, M, N, K, true, true, true};
+  GemmArgs a{xq, nullptr, qweight, nullptr, nullptr, y_i32, M, N, K, true, true, true, workspace, workspace_bytes};
   return run_gemm(a, stream);
 }
 
 int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight, const float* w_scales, const void* bias,
-                    void* y, int64_t M, int64_t N, int64_t K, int8_t* xq_buf, float* a_scales_buf, void* stream) {
+                    void* y, int64_t M, int64_t N, int64_t K, int8_t* xq_buf, float* a_scales_buf, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
   if (int rc = check_dtype(dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
+  if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
   if (M == 0) return ok();
   if (!x || !qweight || !w_scales || !y || !xq_buf || !a_scales_buf)
     return fail(TVQ_E_INVALID, "null pointer argument");
   if (int rc = tvq_act_quant(x, dtype, M, K, 1e-8f, xq_buf, a_scales_buf, stream)) return rc;
-  return tvq_w8a8_gemm(xq_buf, a_scales_buf, qweight, w_scales, bias, y, dtype, M, N, K, stream);
+  return tvq_w8a8_gemm(xq_buf, a_scales_buf, qweight, w_scales, bias, y, dtype, M, N, K, workspace, workspace_bytes,
+                       stream);
 }
 
 int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps, void* y, int8_t* xq, float* a_scales,

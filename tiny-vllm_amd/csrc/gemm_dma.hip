@@ -1,15 +1,16 @@
-// Instantiations of the LDS-DMA pipelined GEMM and the M/N-bucketed choice
+// Instantiations of the LDS-DMA pipelined GEMM and the M/N/K-bucketed choice
 // among them (used when M > 16 and K % 128 == 0).
 //
 // Table (measured on MI355X over the BASELINE shapes; tile = BM x BN, waves,
 // ring depth S, MFMA shape):
 //   W8A8  >= 256 256x256 tiles          256x256, 8 waves (2x4), S=2, 32x32x32 i8
 //         >= 200 256x128 tiles          256x128, 8 waves (4x2), S=2, 32x32x32 i8
-//         M > 256                        64x64,   4 waves,       S=4, 16x16x64 i8
+//         M > 256, or split-K M > 32     64x64,   4 waves,       S=4, 16x16x64 i8
 //         32 < M <= 64, N >= 16384       64x128,  8 waves (2x4), S=4, 16x16x64 i8
 //         otherwise                      32x64,   4 waves,       S=4, 16x16x64 i8
 //   W8A16 >= 200 128x256 tiles          128x256, 8 waves (2x4), S=2, 32x32x16 bf16
 //         M > 256                        64x128,  4 waves,       S=4, 32x32x16
+//         split-K M > 32                 64x64,   4 waves,       S=4, 32x32x16
 //         32 < M <= 64, N >= 16384       64x128,  4 waves,       S=4, 32x32x16
 //         M <= 64                        32x64,   4 waves,       S=4, 16x16x32 bf16
 //         otherwise                      64x64,   4 waves,       S=4, 32x32x16
@@ -20,7 +21,10 @@
 // stage a 2x4-wave 256x256 tile reads 192 KB of fragments and takes 64 KB of
 // DMA writes against 2048 MFMA cycles per SIMD, i.e. ~128 B/clk, the CU's
 // LDS rate. (Fewer, larger wave tiles need 1 wave/SIMD and measured slower.)
-// Small tiles keep >= 256 workgroups in flight at decode-batch M.
+// Split-K: decode-size shapes (M <= 64, N < 16384, K >= 2048) leave most CUs
+// idle with whole-K tiles (e.g. 64 tiles of 64x64 for N = 4096), so with a
+// caller workspace they split K into up to CUs/tiles ranges of >= 8 stages,
+// one work unit per CU (e.g. 8B down_proj at M = 64: 49 -> 22 us W8A16).
 #include "gemm_dma_kernel.h"
 #include "tvq_internal.h"
 
@@ -33,19 +37,62 @@ enum class DmaCfg {
   kI8_256x256, kI8_256x128, kI8_64x64, kI8_64x128, kI8_32x64, kH_128x256, kH_64x128, kH_64x64, kH_32x64
 };
 
+// Tile BM x BN, waves WM x WN, ring depth S, MFMA tile MF, per DmaCfg.
+struct CfgInfo {
+  bool w8a8;
+  int bm, bn, wm, wn, s, mf;
+  const char* name;
+  const char* name_split;  // the same tiles with K split over several workgroups
+};
+constexpr CfgInfo kInfo[] = {
+    {true, 256, 256, 2, 4, 2, 32, "dma_mfma_i8_256x256", "dma_mfma_i8_256x256_splitk"},
+    {true, 256, 128, 4, 2, 2, 32, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk"},
+    {true, 64, 64, 2, 2, 4, 16, "dma_mfma_i8_64x64", "dma_mfma_i8_64x64_splitk"},
+    {true, 64, 128, 2, 4, 4, 16, "dma_mfma_i8_64x128", "dma_mfma_i8_64x128_splitk"},
+    {true, 32, 64, 2, 2, 4, 16, "dma_mfma_i8_32x64", "dma_mfma_i8_32x64_splitk"},
+    {false, 128, 256, 2, 4, 2, 32, "dma_mfma_f16x_128x256", "dma_mfma_f16x_128x256_splitk"},
+    {false, 64, 128, 2, 2, 4, 32, "dma_mfma_f16x_64x128", "dma_mfma_f16x_64x128_splitk"},
+    {false, 64, 64, 2, 2, 4, 32, "dma_mfma_f16x_64x64", "dma_mfma_f16x_64x64_splitk"},
+    {false, 32, 64, 2, 2, 4, 16, "dma_mfma_f16x_32x64", "dma_mfma_f16x_32x64_splitk"},
+};
+
+static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_32x64 + 1, "one entry per DmaCfg");
+static_assert(kInfo[(int)DmaCfg::kI8_32x64].bm == 32 && kInfo[(int)DmaCfg::kH_128x256].bn == 256 &&
+                  !kInfo[(int)DmaCfg::kH_64x64].w8a8 && kInfo[(int)DmaCfg::kI8_64x128].bn == 128,
+              "kInfo follows the DmaCfg order");
+
+template <DmaCfg c>
+constexpr CfgInfo info() {
+  return kInfo[(int)c];
+}
+
+// Tiles with BM <= 64 (decode-size M) may split K.
+template <DmaCfg c>
+constexpr bool splittable() {
+  return info<c>().bm <= 64;
+}
+
 int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
-DmaCfg choose(bool w8a8, int64_t M, int64_t N) {
+// Decode-size shapes whose tiles cannot fill the GPU split K (given a
+// workspace): M <= 64, fewer than 16384 output channels, K >= 2048.
+bool split_shape(int64_t M, int64_t N, int64_t K) { return M <= 64 && N < 16384 && K >= 2048; }
+
+DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
+  const bool split = split_shape(M, N, K);
   if (w8a8) {
     if (tiles(M, N, 256, 256) >= 256) return DmaCfg::kI8_256x256;
     if (tiles(M, N, 256, 128) >= 200) return DmaCfg::kI8_256x128;
-    if (M > 256) return DmaCfg::kI8_64x64;
+    if (M > 256 || (split && M > 32)) return DmaCfg::kI8_64x64;
     if (M > 32 && M <= 64 && N >= 16384) return DmaCfg::kI8_64x128;
     return DmaCfg::kI8_32x64;
   }
   if (tiles(M, N, 128, 256) >= 200) return DmaCfg::kH_128x256;
   if (M > 256) return DmaCfg::kH_64x128;
-  if (M <= 64) return (M > 32 && N >= 16384) ? DmaCfg::kH_64x128 : DmaCfg::kH_32x64;
+  if (M <= 64) {
+    if (split && M > 32) return DmaCfg::kH_64x64;
+    return (M > 32 && N >= 16384) ? DmaCfg::kH_64x128 : DmaCfg::kH_32x64;
+  }
   return DmaCfg::kH_64x64;
 }
 
@@ -57,39 +104,54 @@ int m_major(const GemmArgs& a) {
   return a.N * a.K > xbytes ? 1 : 0;
 }
 
+template <DmaCfg c>
+int splits_of(int64_t M, int64_t N, int64_t K, const void* ws, int64_t ws_bytes) {
+  if constexpr (!splittable<c>()) {
+    return 1;
+  } else {
+    if (!split_shape(M, N, K)) return 1;
+    constexpr CfgInfo i = info<c>();
+    return dma::choose_splits((int)tiles(M, N, i.bm, i.bn), (int)(K / 128), dma::device_cus(), i.bm * i.bn * 4, ws,
+                              ws_bytes);
+  }
+}
+
+int splits_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64_t ws_bytes) {
+  switch (c) {
+#define TVQ_CASE(C) \
+  case DmaCfg::C: return splits_of<DmaCfg::C>(M, N, K, ws, ws_bytes);
+    TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
+    TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64)
+#undef TVQ_CASE
+  }
+  return 1;
+}
+
+template <typename T, bool kRaw, DmaCfg c>
+hipError_t go(const GemmArgs& a, hipStream_t s) {
+  constexpr CfgInfo i = info<c>();
+  const int splits = splits_for(c, a.M, a.N, a.K, a.workspace, a.workspace_bytes);
+  return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, splittable<c>()>(
+      a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), splits,
+      a.workspace, a.workspace_bytes, s);
+}
+
 template <typename T, bool kW8A8, bool kRaw>
 hipError_t run(const GemmArgs& a, hipStream_t s) {
-  const int M = (int)a.M, N = (int)a.N, K = (int)a.K, mm = m_major(a);
-  const int8_t* q = a.qweight;
   if constexpr (kW8A8) {
-    const auto* x = a.x;
-    const auto* as = a.a_scales;
-    switch (choose(true, a.M, a.N)) {
-      case DmaCfg::kI8_256x256:
-        return launch_dma<T, true, kRaw, 256, 256, 2, 4, 2, 32>(x, as, q, a.scales, a.bias, a.y, M, N, K, 8, mm, s);
-      case DmaCfg::kI8_256x128:
-        return launch_dma<T, true, kRaw, 256, 128, 4, 2, 2, 32>(x, as, q, a.scales, a.bias, a.y, M, N, K, 8, mm, s);
-      case DmaCfg::kI8_64x64:
-        return launch_dma<T, true, kRaw, 64, 64, 2, 2, 4, 16>(x, as, q, a.scales, a.bias, a.y, M, N, K, 8, mm, s);
-      case DmaCfg::kI8_64x128:
-        return launch_dma<T, true, kRaw, 64, 128, 2, 4, 4, 16>(x, as, q, a.scales, a.bias, a.y, M, N, K, 8, mm, s);
-      default:
-        return launch_dma<T, true, kRaw, 32, 64, 2, 2, 4, 16>(x, as, q, a.scales, a.bias, a.y, M, N, K, 8, mm, s);
+    switch (choose(true, a.M, a.N, a.K)) {
+      case DmaCfg::kI8_256x256: return go<T, kRaw, DmaCfg::kI8_256x256>(a, s);
+      case DmaCfg::kI8_256x128: return go<T, kRaw, DmaCfg::kI8_256x128>(a, s);
+      case DmaCfg::kI8_64x64: return go<T, kRaw, DmaCfg::kI8_64x64>(a, s);
+      case DmaCfg::kI8_64x128: return go<T, kRaw, DmaCfg::kI8_64x128>(a, s);
+      default: return go<T, kRaw, DmaCfg::kI8_32x64>(a, s);
     }
   } else {
-    switch (choose(false, a.M, a.N)) {
-      case DmaCfg::kH_128x256:
-        return launch_dma<T, false, false, 128, 256, 2, 4, 2, 32>(a.x, nullptr, q, a.scales, a.bias, a.y, M, N, K, 8,
-                                                                  mm, s);
-      case DmaCfg::kH_64x128:
-        return launch_dma<T, false, false, 64, 128, 2, 2, 4, 32>(a.x, nullptr, q, a.scales, a.bias, a.y, M, N, K, 8,
-                                                                 mm, s);
-      case DmaCfg::kH_32x64:
-        return launch_dma<T, false, false, 32, 64, 2, 2, 4, 16>(a.x, nullptr, q, a.scales, a.bias, a.y, M, N, K, 8,
-                                                                mm, s);
-      default:
-        return launch_dma<T, false, false, 64, 64, 2, 2, 4, 32>(a.x, nullptr, q, a.scales, a.bias, a.y, M, N, K, 8, mm,
-                                                                s);
+    switch (choose(false, a.M, a.N, a.K)) {
+      case DmaCfg::kH_128x256: return go<T, false, DmaCfg::kH_128x256>(a, s);
+      case DmaCfg::kH_64x128: return go<T, false, DmaCfg::kH_64x128>(a, s);
+      case DmaCfg::kH_32x64: return go<T, false, DmaCfg::kH_32x64>(a, s);
+      default: return go<T, false, DmaCfg::kH_64x64>(a, s);
     }
   }
 }
@@ -98,18 +160,14 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
 
 bool dma_shape_ok(int64_t K) { return K % 128 == 0; }
 
-const char* dma_path_name(bool w8a8, int64_t M, int64_t N) {
-  switch (choose(w8a8, M, N)) {
-    case DmaCfg::kI8_256x256: return "dma_mfma_i8_256x256";
-    case DmaCfg::kI8_256x128: return "dma_mfma_i8_256x128";
-    case DmaCfg::kI8_64x64: return "dma_mfma_i8_64x64";
-    case DmaCfg::kI8_64x128: return "dma_mfma_i8_64x128";
-    case DmaCfg::kI8_32x64: return "dma_mfma_i8_32x64";
-    case DmaCfg::kH_128x256: return "dma_mfma_f16x_128x256";
-    case DmaCfg::kH_64x128: return "dma_mfma_f16x_64x128";
-    case DmaCfg::kH_32x64: return "dma_mfma_f16x_32x64";
-    default: return "dma_mfma_f16x_64x64";
-  }
+int dma_splits(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes) {
+  static char probe;  // any non-null address: only the size is consulted
+  return splits_for(choose(w8a8, M, N, K), M, N, K, workspace_bytes > 0 ? &probe : nullptr, workspace_bytes);
+}
+
+const char* dma_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes) {
+  const CfgInfo& i = kInfo[(int)choose(w8a8, M, N, K)];
+  return dma_splits(w8a8, M, N, K, workspace_bytes) > 1 ? i.name_split : i.name;
 }
 
 hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream) {

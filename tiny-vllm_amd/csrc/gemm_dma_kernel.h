@@ -45,6 +45,16 @@
 // It stages each wave's MF-row slice of its output through a wave-private
 // area of the idle ring slot S-1 and writes whole row segments of 16-byte
 // stores.
+//
+// Split-K (decode-size M, when there are fewer tiles than resident
+// workgroups): each tile's k-stages are cut into `splits` contiguous ranges
+// and the grid walks (range, tile) work units. A unit writes its raw
+// accumulators (int32 or fp32) to the caller's workspace as a register image
+// with device-scope stores, waits for them to complete and bumps the tile's
+// counter; the unit that arrives last sums all images in range order (so the
+// result does not depend on arrival order; int32 sums are exact) and runs the
+// normal epilogue, then returns the counter to zero. The counters must be
+// zero when a call starts and are zero again when it ends.
 #pragma once
 
 #include <type_traits>
@@ -81,6 +91,11 @@ __device__ __forceinline__ void wait_stage(int ahead) {
   }
 }
 
+// Split-K workspace layout: tile counters (int32) first, then the partial
+// accumulator images, BM*BN 4-byte values per (tile, range).
+constexpr int64_t kSplitCntBytes = 64 * 1024;
+constexpr int kSplitMaxTiles = (int)(kSplitCntBytes / 4);
+
 template <bool kW8A8, int BM, int BN, int WM, int WN, int S, int MF>
 struct Cfg {
   static constexpr int kThreads = 64 * WM * WN;
@@ -97,7 +112,7 @@ struct Cfg {
   static constexpr int FM = TM / MF, FN = TN / MF;        // MFMA tiles per wave
   static constexpr int kEpiBytes = MF * TN * 2;           // per-wave staging: MF rows x TN 16-bit outputs
   static constexpr int kScN = BM + 2 * BN;                // per-tile a_scales | w_scales | bias (fp32, in LDS)
-  static constexpr int kLdsBytes = kRingBytes + kScN * 4;
+  static constexpr int kLdsBytes = kRingBytes + kScN * 4 + 16;   // + the split-K "last unit" flag
   static_assert(MF == 16 || MF == 32, "MFMA tile is 16x16 or 32x32");
   static_assert(kBlkStage % kWaves == 0, "stage blocks must split evenly over waves");
   static_assert(TM % MF == 0 && TN % MF == 0, "wave tile must be a multiple of the MFMA tile");
@@ -180,14 +195,15 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
   }
 }
 
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF>
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, bool kSplit>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
                                                                 const float* __restrict__ ws,
                                                                 const uint16_t* __restrict__ bias,
                                                                 void* __restrict__ yv, int M, int N, int K,
-                                                                int group, int m_major) {
+                                                                int group, int m_major, int splits,
+                                                                char* __restrict__ wsp) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
   using Acc = typename std::conditional<
       MF == 32, typename std::conditional<kW8A8, i32x16, f32x16>::type,
@@ -202,7 +218,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int total = tiles_m * tiles_n;
-  const int nk = K / C::kKStage;
+  const int units = total * splits;
+  const int nk_all = K / C::kKStage;
+  const int nk_per = (nk_all + splits - 1) / splits;   // k-stages per split range
+  // Work unit u -> tile u % total, k range u / total (range-major, so units
+  // that run together share the range's activation panel).
+  auto unit_coords = [&](int u, int& tm_, int& tn_, int& tl_, int& sk_, int& kb_, int& kn_) {
+    tl_ = u % total;
+    sk_ = u / total;
+    tile_coords(tl_, tiles_m, tiles_n, group, m_major, tm_, tn_);
+    kb_ = sk_ * nk_per;
+    kn_ = max(0, min(nk_all, kb_ + nk_per) - kb_);
+  };
 
   // ---- per-lane DMA sources for this wave's blocks ----------------------
   // Each source is a wave-uniform tile base (scalar registers) plus a 32-bit
@@ -211,9 +238,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   const char* xbase = static_cast<const char*>(xv);
   int soff[C::kLPW];
   const int drho = lane >> 3;             // row within the 8-row block
-  auto set_sources = [&](int m0, int n0) {
-    wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K;
-    xbase = static_cast<const char*>(xv) + (int64_t)m0 * K * (kW8A8 ? 1 : 2);
+  auto set_sources = [&](int m0, int n0, int kb) {
+    wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K + (int64_t)kb * C::kKStage;
+    xbase = static_cast<const char*>(xv) + ((int64_t)m0 * K + (int64_t)kb * C::kKStage) * (kW8A8 ? 1 : 2);
 #pragma unroll
     for (int j = 0; j < C::kLPW; ++j) {
       const int b = j * C::kWaves + wave;
@@ -296,10 +323,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     }
   };
 
-  int tile = blockIdx.x;
-  int tm, tn;
-  tile_coords(tile, tiles_m, tiles_n, group, m_major, tm, tn);
-  set_sources(tm * BM, tn * BN);
+  int unit = blockIdx.x;
+  int tm, tn, tl, sk, kb, nk;
+  unit_coords(unit, tm, tn, tl, sk, kb, nk);
+  set_sources(tm * BM, tn * BN, kb);
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
     if (s < nk) issue(s);
@@ -308,20 +335,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   while (true) {
     const int n0 = tn * BN;
     const int m0 = tm * BM;
+    const int cur_tl = tl, cur_sk = sk, cur_nk = nk;
     Acc acc[C::FN][C::FM];
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
       for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
 
-    for (int kt = 0; kt < nk; ++kt) {
-      wait_stage<C::kLPW, S>(min(S - 2, nk - 1 - kt));
+    for (int kt = 0; kt < cur_nk; ++kt) {
+      wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 1 - kt));
       barrier();
       if constexpr (!kRaw) {
         // after the barrier: the previous tile's epilogue no longer reads them
         if (kt == 0) store_scales();
       }
-      if (kt + S - 1 < nk) issue(kt + S - 1);
+      if (kt + S - 1 < cur_nk) issue(kt + S - 1);
 
       const char* wst = smem + (kt % S) * C::kStageBytes + wn * C::FN * kWFrag;
       const char* xst = smem + (kt % S) * C::kStageBytes + C::kWBlk * 1024 + wm * C::FM * kXFrag;
@@ -397,16 +425,73 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     // Every wave has consumed its last fragments: the ring is free.
     barrier();
     // ---- next tile: start its operand stream before this tile's stores ----
-    const int next = tile + (int)gridDim.x;
-    const bool more = next < total;
+    const int next = unit + (int)gridDim.x;
+    const bool more = next < units;
     if (more) {
-      tile = next;
-      tile_coords(tile, tiles_m, tiles_n, group, m_major, tm, tn);
-      set_sources(tm * BM, tn * BN);
+      unit = next;
+      unit_coords(unit, tm, tn, tl, sk, kb, nk);
+      set_sources(tm * BM, tn * BN, kb);
 #pragma unroll
       for (int s = 0; s < S - 1; ++s)
         if (s < nk) issue(s);
       if constexpr (!kRaw) load_scales(tm * BM, tn * BN);
+    }
+
+    // ---- split-K fixup ------------------------------------------------------
+    // The images are written and read with device-scope (agent) atomic stores
+    // and loads, which bypass the per-XCD L2 and meet at the coherent memory
+    // side; so completing the stores (vmcnt 0) before the counter update is
+    // the whole release, and no L2 write-back or invalidate is needed.
+    if (kSplit && splits > 1) {
+      using E = typename std::conditional<kW8A8, int32_t, float>::type;
+      constexpr int kQ4 = kAccN / 4;
+      E* part = reinterpret_cast<E*>(wsp + kSplitCntBytes);
+      int* cnt = reinterpret_cast<int*>(wsp);
+      int* last_flag = reinterpret_cast<int*>(smem + C::kRingBytes + C::kScN * 4);
+      // Register image: value e of 4-value group q of fragment (i, j) of this
+      // wave at (((wave * FN + i) * FM + j) * kQ4 + q) * 256 + 64 * e + lane,
+      // so each store instruction of a wave covers 256 contiguous bytes.
+      auto img = [&](int s, int i, int j, int q, int e) {
+        return part + ((int64_t)cur_tl * splits + s) * (BM * BN) + (((wave * C::FN + i) * C::FM + j) * kQ4 + q) * 256 +
+               64 * e + lane;
+      };
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j)
+#pragma unroll
+          for (int q = 0; q < kQ4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              __hip_atomic_store(img(cur_sk, i, j, q, e), (E)acc[i][j][4 * q + e], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      wait_vm<0>();
+      __syncthreads();
+      if (threadIdx.x == 0)
+        *last_flag = __hip_atomic_fetch_add(cnt + cur_tl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+      __syncthreads();
+      if (!*last_flag) {
+        if (!more) break;
+        continue;
+      }
+      // Sum every range's image (this unit's own included, re-read so that the
+      // order is the range order whichever unit finishes last).
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
+      for (int s = 0; s < splits; ++s) {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+          for (int j = 0; j < C::FM; ++j)
+#pragma unroll
+            for (int q = 0; q < kQ4; ++q)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                acc[i][j][4 * q + e] += __hip_atomic_load(img(s, i, j, q, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (threadIdx.x == 0) __hip_atomic_exchange(cnt + cur_tl, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- epilogue -----------------------------------------------------------
@@ -503,9 +588,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   }
 }
 
-// Workgroups one CU holds for a given LDS footprint, times the CU count of the
-// current device (cached per device): the persistent grid size.
-inline int resident_workgroups(int lds_bytes) {
+// CU count of the current device (cached per device; 0 without a device).
+inline int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
@@ -514,16 +598,38 @@ inline int resident_workgroups(int lds_bytes) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
     cus[dev] = n;
   }
+  return cus[dev];
+}
+
+// Workgroups one CU holds for a given LDS footprint, times the CU count: the
+// persistent grid size.
+inline int resident_workgroups(int lds_bytes) {
   const int per_cu = lds_bytes > 0 ? (160 * 1024) / lds_bytes : 1;
-  return cus[dev] * (per_cu > 0 ? per_cu : 1);
+  return device_cus() * (per_cu > 0 ? per_cu : 1);
 }
 
 // Host-side launcher for one configuration.
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF>
+// Number of split-K ranges for a launch: as many as keep the work units
+// within one per CU (more units than CUs measured slower: a second round, or
+// two units sharing a CU's load bandwidth), at least kMinStages k-stages per
+// range, and a workspace that holds every range's accumulator image
+// (1 = no split).
+inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void* wsp, int64_t ws_bytes) {
+  constexpr int kMinStages = 8, kMaxSplits = 16;
+  if (wsp == nullptr || cus <= 0 || tiles <= 0 || tiles > kSplitMaxTiles) return 1;
+  int s = min(cus / tiles, min(nk / kMinStages, kMaxSplits));
+  while (s > 1 && kSplitCntBytes + (int64_t)tiles * s * tile_bytes > ws_bytes) --s;
+  if (s <= 1) return 1;
+  const int per = (nk + s - 1) / s;  // every range non-empty
+  return (nk + per - 1) / per;
+}
+
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, bool kSplit>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
-                      int M, int N, int K, int group, int m_major, hipStream_t stream) {
+                      int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
+                      hipStream_t stream) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
-  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, kSplit>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -532,11 +638,18 @@ hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const f
     attr_set = true;
   }
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  int grid = tiles;
+  // The kernel writes tiles * splits images and `tiles` counters into the
+  // workspace: anything that does not fit runs unsplit.
+  if (!kSplit || wsp == nullptr || splits < 1 || tiles > kSplitMaxTiles ||
+      kSplitCntBytes + (int64_t)tiles * splits * (BM * BN * 4) > ws_bytes)
+    splits = 1;
+  const int units = tiles * splits;
   const int resident = resident_workgroups(C::kLdsBytes);
-  if (resident > 0 && tiles > resident) grid = resident - resident % 8;  // keep whole XCD rounds
+  int grid = units;
+  if (resident > 0 && units > resident) grid = resident - resident % 8;  // keep whole XCD rounds
   kern<<<dim3(grid), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias),
-                                                                 y, M, N, K, group, m_major);
+                                                                 y, M, N, K, group, m_major, splits,
+                                                                 static_cast<char*>(wsp));
   return hipGetLastError();
 }
 

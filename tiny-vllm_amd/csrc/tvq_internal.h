@@ -26,6 +26,8 @@ struct GemmArgs {
   bool w8a8;
   bool bf16;     // activation (W8A16) / output (W8A8) element type
   bool raw_i32;  // W8A8 only: write the int32 accumulator instead of y
+  void* workspace = nullptr;    // split-K workspace (counters zero on entry), or nullptr
+  int64_t workspace_bytes = 0;
 };
 
 bool act_quant_vec_ok(const void* x, const void* xq, int64_t K);
@@ -56,7 +58,10 @@ hipError_t launch_tiled(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_generic(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream);
 bool dma_shape_ok(int64_t K);
-const char* dma_path_name(bool w8a8, int64_t M, int64_t N);
+// Path name, with a "_splitk" suffix when a workspace of the given size makes
+// the launch split K (which needs the device: without one it never splits).
+const char* dma_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes);
+int dma_splits(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes);
 
 hipError_t launch_stream(const GemmArgs& a, hipStream_t stream);
 bool stream_shape_ok(int64_t M, int64_t N, int64_t K);

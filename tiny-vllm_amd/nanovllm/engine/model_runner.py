@@ -96,6 +96,10 @@ class ModelRunner:
         else:
             random_init_(self.model, config.seed, device=device)
         self.model.eval()
+        if device == "cuda":
+            # the split-K GEMM workspace must exist before any graph capture
+            from nanovllm.quantization import _hip
+            _hip.gemm_workspace(torch.device("cuda", 0))
         self._allocate_kv_cache()
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         if device == "cuda" and not config.enforce_eager:

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_NAME = "libtinyvllm_quant.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OP_ACT_QUANT = 0
 OP_W8A16 = 1
@@ -37,10 +37,11 @@ SYMBOLS = (
     ("tvq_last_error", ctypes.c_char_p, ()),
     ("tvq_select_path", ctypes.c_char_p, (_INT, _I64, _I64, _I64, _INT)),
     ("tvq_act_quant", _INT, (_VP, _INT, _I64, _I64, ctypes.c_float, _VP, _VP, _VP)),
-    ("tvq_w8a16_gemm", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP)),
-    ("tvq_w8a8_gemm", _INT, (_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP)),
-    ("tvq_w8a8_gemm_i32", _INT, (_VP, _VP, _VP, _I64, _I64, _I64, _VP)),
-    ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP)),
+    ("tvq_w8a16_gemm", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _I64, _VP)),
+    ("tvq_w8a8_gemm", _INT, (_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP, _I64, _VP)),
+    ("tvq_w8a8_gemm_i32", _INT, (_VP, _VP, _VP, _I64, _I64, _I64, _VP, _I64, _VP)),
+    ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _I64, _VP)),
+    ("tvq_gemm_workspace_bytes", _I64, ()),
     ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_qk_norm_rope", _INT, (_VP, _I64, _VP, _VP, _VP, _VP, _VP, ctypes.c_float, _I64, _INT, _INT, _INT, _I64,
@@ -133,6 +134,31 @@ def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
     return dev
 
 
+_WORKSPACES: dict[int, torch.Tensor] = {}
+
+
+def gemm_workspace(device: torch.device) -> torch.Tensor:
+    """The device's split-K GEMM workspace: allocated zero-filled on first use
+    and shared by every GEMM call on the device (the calls are ordered on the
+    current stream; each leaves the workspace ready for the next). Allocate it
+    before capturing HIP graphs, so captured and eager calls split alike."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACES.get(idx)
+    if ws is None:
+        _require(not torch.cuda.is_current_stream_capturing(),
+                 "the GEMM workspace must be allocated before HIP-graph capture (call gemm_workspace(device))")
+        ws = torch.zeros(load_library().tvq_gemm_workspace_bytes(), dtype=torch.uint8, device=device)
+        _WORKSPACES[idx] = ws
+    return ws
+
+
+def _ws(dev: torch.device, split_k: bool) -> tuple[int | None, int]:
+    if not split_k:
+        return None, 0
+    ws = gemm_workspace(dev)
+    return ws.data_ptr(), ws.numel()
+
+
 def select_path(op: int, m: int, n: int, k: int, dtype: torch.dtype = torch.bfloat16) -> str:
     """Kernel path name for an op and shape (M-bucketed dispatch)."""
     res = load_library().tvq_select_path(op, m, n, k, _TORCH_TO_TVQ.get(dtype, DTYPE_BF16))
@@ -173,7 +199,7 @@ def _check_weight(qweight: torch.Tensor, scales: torch.Tensor, bias: torch.Tenso
 
 
 def w8a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
-               bias: torch.Tensor | None = None) -> torch.Tensor:
+               bias: torch.Tensor | None = None, split_k: bool = True) -> torch.Tensor:
     """y[M,N] = x[M,K] @ (qweight * scales[:,None])^T + bias, on the GPU."""
     lib = load_library()
     dev = _require_gpu(x, qweight, scales, bias)
@@ -186,13 +212,14 @@ def w8a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
         return y
     with torch.cuda.device(dev):
         rc = lib.tvq_w8a16_gemm(x.data_ptr(), _TORCH_TO_TVQ[x.dtype], qweight.data_ptr(), scales.data_ptr(),
-                                _ptr(bias), y.data_ptr(), m, n, k, _stream(dev))
+                                _ptr(bias), y.data_ptr(), m, n, k, *_ws(dev, split_k), _stream(dev))
     _check(rc, "tvq_w8a16_gemm")
     return y
 
 
 def w8a8_gemm(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
-              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16,
+              split_k: bool = True) -> torch.Tensor:
     """y = ((x_q @ qweight^T) * a_scales[:,None]) * w_scales[None,:] + bias, int32 accumulation."""
     lib = load_library()
     dev = _require_gpu(x_q, a_scales, qweight, w_scales, bias)
@@ -207,12 +234,13 @@ def w8a8_gemm(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.Tensor, 
         return y
     with torch.cuda.device(dev):
         rc = lib.tvq_w8a8_gemm(x_q.data_ptr(), a_scales.data_ptr(), qweight.data_ptr(), w_scales.data_ptr(),
-                               _ptr(bias), y.data_ptr(), _TORCH_TO_TVQ[out_dtype], m, n, k, _stream(dev))
+                               _ptr(bias), y.data_ptr(), _TORCH_TO_TVQ[out_dtype], m, n, k, *_ws(dev, split_k),
+                               _stream(dev))
     _check(rc, "tvq_w8a8_gemm")
     return y
 
 
-def w8a8_gemm_i32(x_q: torch.Tensor, qweight: torch.Tensor) -> torch.Tensor:
+def w8a8_gemm_i32(x_q: torch.Tensor, qweight: torch.Tensor, split_k: bool = True) -> torch.Tensor:
     """The exact int32 accumulator x_q @ qweight^T of the W8A8 path."""
     lib = load_library()
     dev = _require_gpu(x_q, qweight)
@@ -225,13 +253,14 @@ def w8a8_gemm_i32(x_q: torch.Tensor, qweight: torch.Tensor) -> torch.Tensor:
     if m == 0:
         return y
     with torch.cuda.device(dev):
-        rc = lib.tvq_w8a8_gemm_i32(x_q.data_ptr(), qweight.data_ptr(), y.data_ptr(), m, n, k, _stream(dev))
+        rc = lib.tvq_w8a8_gemm_i32(x_q.data_ptr(), qweight.data_ptr(), y.data_ptr(), m, n, k, *_ws(dev, split_k),
+                                   _stream(dev))
     _check(rc, "tvq_w8a8_gemm_i32")
     return y
 
 
 def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
-                bias: torch.Tensor | None = None) -> torch.Tensor:
+                bias: torch.Tensor | None = None, split_k: bool = True) -> torch.Tensor:
     """Fused per-token activation quantization + W8A8 GEMM; output in x.dtype."""
     lib = load_library()
     dev = _require_gpu(x, qweight, w_scales, bias)
@@ -246,7 +275,8 @@ def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
     a_s = torch.empty((m,), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         rc = lib.tvq_w8a8_linear(x.data_ptr(), _TORCH_TO_TVQ[x.dtype], qweight.data_ptr(), w_scales.data_ptr(),
-                                 _ptr(bias), y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(), _stream(dev))
+                                 _ptr(bias), y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(),
+                                 *_ws(dev, split_k), _stream(dev))
     _check(rc, "tvq_w8a8_linear")
     return y
 
