@@ -173,6 +173,34 @@ def test_w8a8_fused_linear_matches_two_step(hiplib):
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
 
 
+@pytest.mark.parametrize("shape", [(256, 4096, 1024), (17, 1000, 1024), (100, 4096, 2048), (64, 6144, 1024), (96, 2048, 512),
+                                   (257, 520, 1024), (33, 24576, 1024), (40, 1024, 2048), (8, 4096, 1024)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_w8a8_linear_buffers_and_output(hiplib, shape, dtype):
+    """tvq_w8a8_linear fills the caller's xq / a_scales buffers exactly as
+    tvq_act_quant does and its output equals act-quant + tvq_w8a8_gemm bit
+    for bit (skinny, DMA and split-K GEMM paths)."""
+    from nanovllm.quantization import _hip
+    m, n, k = shape
+    _log_case(test="w8a8_linear_buffers", m=m, n=n, k=k, dtype=dtype)
+    d = _dev()
+    x = make_activations(m, k, seed=m + n + k, dtype=dtype).to(d)
+    q, w_s = (t.to(d) for t in make_weights(n, k, seed=n + 1))
+    y = torch.empty((m, n), dtype=dtype, device=d)
+    xq = torch.full((m, k), 99, dtype=torch.int8, device=d)
+    a_s = torch.full((m,), -1.0, dtype=torch.float32, device=d)
+    ws = _hip.gemm_workspace(d)
+    rc = hiplib.tvq_w8a8_linear(x.data_ptr(), _hip._TORCH_TO_TVQ[dtype], q.data_ptr(), w_s.data_ptr(), None,
+                                y.data_ptr(), m, n, k, xq.data_ptr(), a_s.data_ptr(), ws.data_ptr(), ws.numel(),
+                                torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, hiplib.tvq_last_error()
+    xq_ref, as_ref = _hip.act_quant(x)
+    assert torch.equal(xq, xq_ref)
+    assert torch.equal(a_s.view(torch.int32), as_ref.view(torch.int32))
+    y_ref = _hip.w8a8_gemm(xq_ref, as_ref, q, w_s, None, dtype)
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
 # ---------------------------------------------------------------- W8A16
 
 def _w8a16_check(y, x, q, s, bias=None):

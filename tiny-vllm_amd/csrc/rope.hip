@@ -9,9 +9,11 @@
 // with fp32 temporaries, by one launch that reads q and k once from the packed
 // qkv projection output and writes them once.
 //
-// One wave per (token, head), head_dim D = 128: lane i holds x[i] and
-// x[i + 64], which are exactly the pair the rotate-half rotation mixes, so
-// the rotation is lane-local; the RMS statistic is one wave reduction.
+// Sixteen lanes per (token, head), head_dim D = 128: lane j of the group
+// holds x[4j..4j+3] and x[64+4j..64+4j+3], exactly the pairs the rotate-half
+// rotation mixes, so the rotation is lane-local, every access is 8 bytes per
+// lane (16 for the fp32 cos/sin rows) and the RMS statistic is a 16-lane
+// reduction. Four heads per wave.
 // Rounding follows the reference step by step:
 //   n  = round(x * rsqrt(mean(x^2) + eps))     (fp32, IEEE sqrt and divide)
 //   n  = round(n * w)                           (bf16 x bf16 -> one rounding)
@@ -31,10 +33,28 @@ namespace tvq {
 namespace {
 
 constexpr int kD = 128;
+constexpr int kGroup = 16;                  // lanes per head
+constexpr int kItemsPerBlock = 256 / kGroup;
 
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+__device__ __forceinline__ float group_sum(float v) {
+  for (int off = kGroup / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kGroup);
   return v;
+}
+
+// Four 16-bit values <-> floats.
+template <typename T>
+__device__ __forceinline__ void unpack4(u32x2 w, float (&f)[4]) {
+  f[0] = to_float<T>((uint16_t)w.x);
+  f[1] = to_float<T>((uint16_t)(w.x >> 16));
+  f[2] = to_float<T>((uint16_t)w.y);
+  f[3] = to_float<T>((uint16_t)(w.y >> 16));
+}
+template <typename T>
+__device__ __forceinline__ u32x2 pack4(const float (&f)[4]) {
+  u32x2 w;
+  w.x = (uint32_t)from_float<T>(f[0]) | ((uint32_t)from_float<T>(f[1]) << 16);
+  w.y = (uint32_t)from_float<T>(f[2]) | ((uint32_t)from_float<T>(f[3]) << 16);
+  return w;
 }
 
 template <typename T, bool kNorm>
@@ -49,11 +69,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
                                                            uint16_t* __restrict__ v_cache,
                                                            const int64_t* __restrict__ slots, int num_slots,
                                                            int max_len) {
-  const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int j = threadIdx.x & (kGroup - 1);
+  const int64_t item = (int64_t)blockIdx.x * kItemsPerBlock + (threadIdx.x / kGroup);
   const bool store = k_cache != nullptr;
   const int heads = Hq + Hkv + (store ? Hkv : 0);
-  if (item >= (int64_t)T_ * heads) return;
+  if (item >= (int64_t)T_ * heads) return;  // whole 16-lane groups leave together
   const int64_t t = item / heads;
   const int h = (int)(item % heads);
   const bool is_q = h < Hq;
@@ -67,35 +87,51 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
     if (slot >= 0 && slot < num_slots && pos >= 0 && pos < max_len)
       cache_row = (h < Hq + Hkv ? k_cache : v_cache) + ((slot * Hkv + kvh) * (int64_t)max_len + pos) * kD;
   }
+  const u32x2 lo = *reinterpret_cast<const u32x2*>(src + 4 * j);
+  const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 64 + 4 * j);
   if (h >= Hq + Hkv) {  // value head: copy to the cache only
     if (cache_row) {
-      cache_row[lane] = src[lane];
-      cache_row[lane + 64] = src[lane + 64];
+      *reinterpret_cast<u32x2*>(cache_row + 4 * j) = lo;
+      *reinterpret_cast<u32x2*>(cache_row + 64 + 4 * j) = hi;
     }
     return;
   }
-  float x1 = to_float<T>(src[lane]);
-  float x2 = to_float<T>(src[lane + 64]);
+  float x1[4], x2[4];
+  unpack4<T>(lo, x1);
+  unpack4<T>(hi, x2);
   if constexpr (kNorm) {
-    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+    ss = group_sum(ss);
     const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)kD) + eps));
     const uint16_t* w = is_q ? qw : kw;
-    x1 = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x1 * r)) * to_float<T>(w[lane])));
-    x2 = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x2 * r)) * to_float<T>(w[lane + 64])));
+    float w1[4], w2[4];
+    unpack4<T>(*reinterpret_cast<const u32x2*>(w + 4 * j), w1);
+    unpack4<T>(*reinterpret_cast<const u32x2*>(w + 64 + 4 * j), w2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x1[e] = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x1[e] * r)) * w1[e]));
+      x2[e] = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x2[e] * r)) * w2[e]));
+    }
   }
   int64_t p = positions[t];
   p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
-  const float c = cos_t[p * (kD / 2) + lane];
-  const float s = sin_t[p * (kD / 2) + lane];
-  const float y1 = x1 * c - x2 * s;
-  const float y2 = x2 * c + x1 * s;
+  const f32x4 c = *reinterpret_cast<const f32x4*>(cos_t + p * (kD / 2) + 4 * j);
+  const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + p * (kD / 2) + 4 * j);
+  float y1[4], y2[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y1[e] = x1[e] * c[e] - x2[e] * sn[e];
+    y2[e] = x2[e] * c[e] + x1[e] * sn[e];
+  }
   uint16_t* dst = is_q ? q_out + (t * Hq + h) * kD : k_out + (t * Hkv + (h - Hq)) * kD;
-  const uint16_t o1 = from_float<T>(y1), o2 = from_float<T>(y2);
-  dst[lane] = o1;
-  dst[lane + 64] = o2;
+  const u32x2 o1 = pack4<T>(y1), o2 = pack4<T>(y2);
+  *reinterpret_cast<u32x2*>(dst + 4 * j) = o1;
+  *reinterpret_cast<u32x2*>(dst + 64 + 4 * j) = o2;
   if (cache_row) {
-    cache_row[lane] = o1;
-    cache_row[lane + 64] = o2;
+    *reinterpret_cast<u32x2*>(cache_row + 4 * j) = o1;
+    *reinterpret_cast<u32x2*>(cache_row + 64 + 4 * j) = o2;
   }
 }
 
@@ -106,7 +142,7 @@ hipError_t launch_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_
                                int Hq, int Hkv, int max_pos, void* q_out, void* k_out, void* k_cache, void* v_cache,
                                const int64_t* slots, int num_slots, int max_len, bool bf16, hipStream_t stream) {
   const int64_t items = T_ * (Hq + Hkv + (k_cache ? Hkv : 0));
-  const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+  const dim3 grid((unsigned)((items + kItemsPerBlock - 1) / kItemsPerBlock)), block(256);
   auto X = static_cast<const uint16_t*>(qkv);
   auto QW = static_cast<const uint16_t*>(q_weight);
   auto KW = static_cast<const uint16_t*>(k_weight);
