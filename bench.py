@@ -273,6 +273,34 @@ def cpu_baseline(budget_s=12.0):
                        f"median, torch CPU {torch.__version__} with {threads} threads, ~{budget_s:.0f}s budget")
 
 
+# ---------------------------------------------------------------- profiling one GEMM
+
+def run_profile_case(spec):
+    from nanovllm.quantization import _hip
+    mode, m, n, k = spec.split(",")
+    m, n, k = int(m), int(n), int(k)
+    if mode not in ("w8a8", "w8a16"):
+        raise SystemExit(f"--profile-case: mode must be w8a8 or w8a16, got {mode}")
+    lib = _hip.load_library()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    L = Launcher(lib, dev)
+    x, qs, ss = make_inputs(mode, m, n, k, dev)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    if mode == "w8a8":
+        xq, a_s = _hip.act_quant(x)
+        fns = [L.w8a8(xq, a_s, qs[i % len(qs)], ss[i % len(qs)], y) for i in range(64)]
+    else:
+        fns = [L.w8a16(x, qs[i % len(qs)], ss[i % len(qs)], y) for i in range(64)]
+    g = _graph(fns)
+    for _ in range(8):
+        g.replay()
+    torch.cuda.synchronize()
+    op = _hip.OP_W8A8 if mode == "w8a8" else _hip.OP_W8A16
+    print(json.dumps(dict(profile_case=spec, path=_hip.select_path(op, m, n, k), launches=8 * 64,
+                          weight_copies=len(qs))), flush=True)
+
+
 # ---------------------------------------------------------------- main
 
 def main():
@@ -286,7 +314,13 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--profile-case", default=None, metavar="MODE,M,N,K",
+                    help="profiling run of one GEMM (mode w8a8 or w8a16) for rocprofv3: 8 graph replays of 64 "
+                         "launches over the rotating weight copies; prints nothing but the path")
     args = ap.parse_args()
+    if args.profile_case:
+        run_profile_case(args.profile_case)
+        return
     if args.profile:
         args.no_sweep = args.no_cpu = True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -131,9 +131,17 @@ template <typename T, bool kRaw, DmaCfg c>
 hipError_t go(const GemmArgs& a, hipStream_t s) {
   constexpr CfgInfo i = info<c>();
   const int splits = splits_for(c, a.M, a.N, a.K, a.workspace, a.workspace_bytes);
-  return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, splittable<c>()>(
-      a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), splits,
-      a.workspace, a.workspace_bytes, s);
+  // Unsplit launches use the instantiation without the split-K fixup (fewer
+  // registers; measured ~4 % faster on the M=256 headline shape).
+  if constexpr (splittable<c>()) {
+    if (splits > 1)
+      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, true>(
+          a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), splits,
+          a.workspace, a.workspace_bytes, s);
+  }
+  return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, false>(
+      a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0,
+      s);
 }
 
 template <typename T, bool kW8A8, bool kRaw>

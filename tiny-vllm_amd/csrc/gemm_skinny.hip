@@ -40,12 +40,11 @@ struct SkinnyCfg {
   static constexpr int U = (8 / (RG * MG)) > 0 ? (8 / (RG * MG)) : 1;
 };
 
-template <typename T, bool kW8A8, bool kRaw, int MG, int RG, int kWaves>
+template <typename T, bool kW8A8, bool kRaw, int MG, int RG, int kWaves, int U>
 __global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restrict__ xv, const float* __restrict__ a_scales,
                                                      const int8_t* __restrict__ qw, const float* __restrict__ ws,
                                                      const uint16_t* __restrict__ bias, void* __restrict__ yv,
                                                      int M, int N, int K) {
-  constexpr int U = SkinnyCfg<MG, RG>::U;
   using Acc = typename std::conditional<kW8A8, i32x4, f32x4>::type;
   constexpr int kXRegs = kW8A8 ? 1 : 2;  // 16-byte x vectors per (chunk, m-group)
 
@@ -188,11 +187,11 @@ __global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restr
   }
 }
 
-template <typename T, bool kW8A8, bool kRaw, int MG, int RG, int W>
+template <typename T, bool kW8A8, bool kRaw, int MG, int RG, int W, int U = SkinnyCfg<MG, RG>::U>
 hipError_t launch_w(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)((a.N + 16 * RG - 1) / (16 * RG)));
   const dim3 block(64 * W);
-  skinny_kernel<T, kW8A8, kRaw, MG, RG, W><<<grid, block, 0, stream>>>(
+  skinny_kernel<T, kW8A8, kRaw, MG, RG, W, U><<<grid, block, 0, stream>>>(
       a.x, a.a_scales, a.qweight, a.scales, static_cast<const uint16_t*>(a.bias), a.y, (int)a.M, (int)a.N, (int)a.K);
   return hipGetLastError();
 }
@@ -208,6 +207,11 @@ hipError_t launch_rg(const GemmArgs& a, hipStream_t stream) {
     if (runs > 8) return launch_w<T, kW8A8, kRaw, MG, RG, 16>(a, stream);
   }
   if (a.N >= 16384) return launch_w<T, kW8A8, kRaw, MG, RG, 4>(a, stream);
+  // Short K (<= 1024) with one 16x16 block per wave: runs of 4 chunks keep all
+  // 4 waves busy (measured 3-8 % faster at K = 1024 than 2 busy waves).
+  if constexpr (RG * MG == 1) {
+    if (a.K <= 1024) return launch_w<T, kW8A8, kRaw, MG, RG, 4, 4>(a, stream);
+  }
   if constexpr (RG * MG <= 4) {
     if (runs > 4) return launch_w<T, kW8A8, kRaw, MG, RG, 8>(a, stream);
   }
