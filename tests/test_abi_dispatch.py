@@ -75,7 +75,11 @@ def test_select_path_buckets(hiplib):
     sp = _hip.select_path
     assert sp(_hip.OP_ACT_QUANT, 4, 0, 1024) == "act_quant_vec"
     assert sp(_hip.OP_ACT_QUANT, 4, 0, 100) == "act_quant_scalar"
-    assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "skinny_mfma_f16x_m16"
+    assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "gemv_dot2_f16x"          # M <= 2, K % 1024 == 0
+    assert sp(_hip.OP_W8A8, 2, 4096, 12288) == "gemv_dot4_i8"
+    assert sp(_hip.OP_W8A8, 3, 4096, 12288) == "skinny_mfma_i8_m16"
+    assert sp(_hip.OP_W8A8, 1, 4096, 1040) == "skinny_mfma_i8_m16"     # K % 1024 != 0
+    assert sp(_hip.OP_W8A8, 1, 4096, 16384) == "skinny_mfma_i8_m16"    # K > 12288
     assert sp(_hip.OP_W8A16, 16, 4096, 1024) == "skinny_mfma_f16x_m16"
     assert sp(_hip.OP_W8A16, 64, 4096, 1024) == "dma_mfma_f16x_32x64"     # 16 < M <= 64: DMA tiles
     # split-K shapes (M <= 64, N < 16384, K >= 2048) take 64x64 tiles above M = 32; without a

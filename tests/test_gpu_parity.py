@@ -104,7 +104,7 @@ GEMM_SHAPES = [
     (1, 1024, 12288), (33, 4096, 4096), (7, 200, 2048), (5, 96, 1040), (24, 16384, 512), (64, 16448, 256),
     (9, 20000, 768), (16, 16384, 1024), (40, 16384, 1024), (64, 24576, 256),
     (65, 4096, 1024), (256, 4096, 1024), (512, 1024, 3072), (300, 1030, 2048), (129, 136, 80),
-    (7, 33, 40), (3, 5, 1024),
+    (7, 33, 40), (3, 5, 1024), (2, 4104, 3072), (4, 24576, 4096), (1, 6144, 9216),
 ]
 
 

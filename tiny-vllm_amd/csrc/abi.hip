@@ -70,6 +70,7 @@ int run_gemm(const GemmArgs& a, void* stream) {
     case Path::kTiled: e = launch_tiled(a, (hipStream_t)stream); break;
     case Path::kDma: e = launch_dma_gemm(a, (hipStream_t)stream); break;
     case Path::kStream: e = launch_stream(a, (hipStream_t)stream); break;
+    case Path::kGemv: e = launch_gemv(a, (hipStream_t)stream); break;
     default: e = launch_generic(a, (hipStream_t)stream); break;
   }
   if (e != hipSuccess) return fail(TVQ_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
@@ -81,6 +82,7 @@ int run_gemm(const GemmArgs& a, void* stream) {
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
   if (!aligned) return Path::kGeneric;
+  if (gemv_shape_ok(a.M, a.K)) return Path::kGemv;
   if (a.M <= kSkinnyMaxM) {
     if (a.M > kDmaMinM && dma_shape_ok(a.K)) return Path::kDma;
     return stream_shape_ok(a.M, a.N, a.K) ? Path::kStream : Path::kSkinny;
@@ -90,6 +92,7 @@ Path select_gemm_path(const GemmArgs& a) {
 
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
+  if (gemv_shape_ok(M, K)) return w8a8 ? "gemv_dot4_i8" : "gemv_dot2_f16x";
   if (M > kDmaMinM && dma_shape_ok(K)) return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
   if (M <= kSkinnyMaxM && stream_shape_ok(M, N, K)) {
     static const char* s8[4] = {"stream_mfma_i8_m16", "stream_mfma_i8_m32", "stream_mfma_i8_m48", "stream_mfma_i8_m64"};

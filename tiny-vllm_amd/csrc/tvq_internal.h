@@ -13,6 +13,7 @@ enum class Path : int {
   kTiled = 2,    // M > 64, K % 128 != 0: register-staged double-buffered MFMA tiles
   kDma = 3,      // M > 64, K % 128 == 0: LDS-DMA multi-stage MFMA tiles
   kStream = 4,   // 8 < M <= 64, N >= 16384, K % 256 == 0: weight streaming, LDS-shared activations
+  kGemv = 5,     // M <= 2, K % 1024 == 0: row-contiguous vector-ALU GEMV
 };
 
 struct GemmArgs {
@@ -64,11 +65,14 @@ const char* dma_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t wo
 int dma_splits(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes);
 
 hipError_t launch_stream(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_gemv(const GemmArgs& a, hipStream_t stream);
+bool gemv_shape_ok(int64_t M, int64_t K);
 bool stream_shape_ok(int64_t M, int64_t N, int64_t K);
 
 // Largest M served by the skinny / stream families; above kDmaMinM they are
 // used only when K % 128 != 0 (the DMA tiles need whole 128-k stages).
 constexpr int64_t kSkinnyMaxM = 64;
 constexpr int64_t kDmaMinM = 16;
+constexpr int64_t kGemvMaxM = 2;  // M = 4 measured 20-35 % slower than the skinny MFMA kernel
 
 }  // namespace tvq
