@@ -102,7 +102,7 @@ def test_act_quant_near_ties_bit_exact(hiplib, dtype):
 GEMM_SHAPES = [
     (1, 4096, 1024), (16, 4096, 1024), (17, 1000, 1024), (48, 6144, 1024), (64, 1024, 3072),
     (1, 1024, 12288), (33, 4096, 4096), (7, 200, 2048), (5, 96, 1040), (24, 16384, 512), (64, 16448, 256),
-    (9, 20000, 768), (16, 16384, 1024), (40, 16384, 1024), (64, 24576, 256),
+    (9, 20000, 768), (16, 16384, 1024), (40, 16384, 1024), (64, 24576, 256), (12, 6144, 4096), (16, 4096, 12288),
     (65, 4096, 1024), (256, 4096, 1024), (512, 1024, 3072), (300, 1030, 2048), (129, 136, 80),
     (7, 33, 40), (3, 5, 1024), (2, 4104, 3072), (4, 24576, 4096), (1, 6144, 9216),
 ]

@@ -84,7 +84,7 @@ Path select_gemm_path(const GemmArgs& a) {
   if (!aligned) return Path::kGeneric;
   if (gemv_shape_ok(a.M, a.K)) return Path::kGemv;
   if (a.M <= kSkinnyMaxM) {
-    if (a.M > kDmaMinM && dma_shape_ok(a.K)) return Path::kDma;
+    if (dma_shape_ok(a.K) && (a.M > kDmaMinM || (a.M > 8 && a.N * a.K >= kDmaMidWeights))) return Path::kDma;
     return stream_shape_ok(a.M, a.N, a.K) ? Path::kStream : Path::kSkinny;
   }
   return dma_shape_ok(a.K) ? Path::kDma : Path::kTiled;
@@ -93,7 +93,8 @@ Path select_gemm_path(const GemmArgs& a) {
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
   if (gemv_shape_ok(M, K)) return w8a8 ? "gemv_dot4_i8" : "gemv_dot2_f16x";
-  if (M > kDmaMinM && dma_shape_ok(K)) return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
+  if (M <= kSkinnyMaxM && dma_shape_ok(K) && (M > kDmaMinM || (M > 8 && N * K >= kDmaMidWeights)))
+    return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
   if (M <= kSkinnyMaxM && stream_shape_ok(M, N, K)) {
     static const char* s8[4] = {"stream_mfma_i8_m16", "stream_mfma_i8_m32", "stream_mfma_i8_m48", "stream_mfma_i8_m64"};
     static const char* s16[4] = {"stream_mfma_f16x_m16", "stream_mfma_f16x_m32", "stream_mfma_f16x_m48",

@@ -73,6 +73,10 @@ bool stream_shape_ok(int64_t M, int64_t N, int64_t K);
 // used only when K % 128 != 0 (the DMA tiles need whole 128-k stages).
 constexpr int64_t kSkinnyMaxM = 64;
 constexpr int64_t kDmaMinM = 16;
+// 8 < M <= 16 also takes the DMA tiles (with split-K) when the weights are at
+// least this large: 1.2-1.3x faster than the skinny / stream kernels on the
+// 8B qkv, gate_up and down shapes at M = 16, slower on smaller ones.
+constexpr int64_t kDmaMidWeights = 24ll << 20;
 constexpr int64_t kGemvMaxM = 2;  // M = 4 measured 20-35 % slower than the skinny MFMA kernel
 
 }  // namespace tvq
