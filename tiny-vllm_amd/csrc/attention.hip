@@ -20,7 +20,8 @@
 // (lane li holds dims 8*li .. 8*li+7, so a 256-byte K or V row is one
 // coalesced 16-byte load per lane) with its own online-softmax state for the
 // G query heads that share the kv head. The 16 groups of the workgroup walk
-// positions with stride 16; their states are merged through LDS at the end.
+// positions with stride 16, four positions per step; their states are merged
+// through LDS at the end.
 // HBM traffic is the algorithmic minimum: each K/V row of the sequence is
 // read once (2 * len * D * 2 bytes per kv head).
 #include "tvq_common.h"
@@ -76,14 +77,18 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
         *reinterpret_cast<const u32x4*>(vn + 8 * (tid - 16));
   }
 
-  // 2. per-group online softmax over positions grp, grp+16, ...
+  // 2. per-group online softmax over positions grp, grp+16, ..., four per
+  //    step (their K/V loads in flight together). Logits are kept in the
+  //    log2 domain (scale * log2(e) folded into q) so each exponential is one
+  //    v_exp_f32.
+  constexpr float kLog2e = 1.4426950408889634f;
   float qf[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float t[8];
     unpack8<T>(*reinterpret_cast<const u32x4*>(q + (int64_t)b * q_stride + (g * G + h) * kD + 8 * li), t);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qf[h][i] = t[i] * scale;
+    for (int i = 0; i < 8; ++i) qf[h][i] = t[i] * (scale * kLog2e);
   }
   float m[G], l[G], o[G][8];
 #pragma unroll
@@ -94,36 +99,60 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
     for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
   }
 
-  const int steps = (len + kGroups - 1) / kGroups;
+  constexpr int kPP = 4;  // positions per group per step
+  const int steps = (len + kPP * kGroups - 1) / (kPP * kGroups);
   for (int st = 0; st < steps; ++st) {
-    const int p = st * kGroups + grp;
-    const bool valid = p < len;
-    const bool last = p == len - 1;
-    const int pc = valid ? p : 0;
-    const uint16_t* kp = last ? kn : kc + (int64_t)pc * kD;
-    const uint16_t* vp = last ? vn : vc + (int64_t)pc * kD;
-    float kf[8], vf[8];
-    unpack8<T>(*reinterpret_cast<const u32x4*>(kp + 8 * li), kf);
-    unpack8<T>(*reinterpret_cast<const u32x4*>(vp + 8 * li), vf);
+    const int p0 = st * kPP * kGroups + grp;
+    if (p0 >= len) continue;  // nothing valid this step (whole groups agree)
+    float kf[kPP][8], vf[kPP][8];
+    bool ok[kPP];
+#pragma unroll
+    for (int u = 0; u < kPP; ++u) {
+      const int pu = p0 + u * kGroups;
+      ok[u] = pu < len;
+      const int pc = ok[u] ? pu : p0;
+      const uint16_t* kp = pc == len - 1 ? kn : kc + (int64_t)pc * kD;
+      const uint16_t* vp = pc == len - 1 ? vn : vc + (int64_t)pc * kD;
+      unpack8<T>(*reinterpret_cast<const u32x4*>(kp + 8 * li), kf[u]);
+      unpack8<T>(*reinterpret_cast<const u32x4*>(vp + 8 * li), vf[u]);
+    }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float s = 0.0f;
+      float sc[kPP];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) s = fmaf(qf[h][i], kf[i], s);
-      // reduce over the 16 lanes of the group
-      s += __shfl_xor(s, 8, 16);
-      s += __shfl_xor(s, 4, 16);
-      s += __shfl_xor(s, 2, 16);
-      s += __shfl_xor(s, 1, 16);
-      if (valid) {
-        const float mn = fmaxf(m[h], s);
-        const float corr = expf(m[h] - mn);  // 0 on the first valid position (m = -inf)
-        const float e = expf(s - mn);
-        l[h] = l[h] * corr + e;
+      for (int u = 0; u < kPP; ++u) {
+        float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][i] = fmaf(o[h][i], corr, e * vf[i]);
-        m[h] = mn;
+        for (int i = 0; i < 8; ++i) a = fmaf(qf[h][i], kf[u][i], a);
+        sc[u] = a;
       }
+      // reduce over the 16 lanes of the group
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1)
+#pragma unroll
+        for (int u = 0; u < kPP; ++u) sc[u] += __shfl_xor(sc[u], off, 16);
+      float mn = m[h];
+#pragma unroll
+      for (int u = 0; u < kPP; ++u) {
+        if (!ok[u]) sc[u] = -INFINITY;
+        mn = fmaxf(mn, sc[u]);
+      }
+      const float corr = __builtin_amdgcn_exp2f(m[h] - mn);  // 0 on the first step (m = -inf)
+      float e[kPP], es = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kPP; ++u) {
+        e[u] = __builtin_amdgcn_exp2f(sc[u] - mn);          // 0 past the end
+        es += e[u];
+      }
+      l[h] = fmaf(l[h], corr, es);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = o[h][i] * corr;
+#pragma unroll
+        for (int u = 0; u < kPP; ++u) acc = fmaf(e[u], vf[u][i], acc);
+        o[h][i] = acc;
+      }
+      m[h] = mn;
     }
   }
 
@@ -149,7 +178,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
     float L = 0.0f, acc = 0.0f;
 #pragma unroll
     for (int x = 0; x < kGroups; ++x) {
-      const float w = sm[x][h][1] > 0.0f ? expf(sm[x][h][0] - M) : 0.0f;
+      const float w = sm[x][h][1] > 0.0f ? __builtin_amdgcn_exp2f(sm[x][h][0] - M) : 0.0f;
       L = fmaf(sm[x][h][1], w, L);
       acc = fmaf(so[x][h][d], w, acc);
     }
