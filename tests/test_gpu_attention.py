@@ -117,7 +117,7 @@ def _prefill_ref(q, k, v, lens, scale):
     return out
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8), (24, 4), (6, 2)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_prefill_attention_matches_fp32_reference(hiplib, hq, hkv, dtype):
     from nanovllm.quantization import _hip

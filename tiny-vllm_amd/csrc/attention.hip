@@ -229,9 +229,12 @@ hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* 
 // 64-query blocks (token offset of the sequence, its length, first query of
 // the block), longest work first.
 //
-// One 256-thread workgroup per (query block, query head): each wave owns 16
-// queries; 64-key blocks of K and V (the kv head of the query head) are
-// staged in LDS, K row-major and V transposed. Both products run on
+// One workgroup per (query block, group of G query heads sharing a kv head;
+// G = 4, 2 or 1 divides Hq/Hkv), 4 waves per head: each wave owns 16 queries
+// of one head;
+// 64-key blocks of K and V are staged once for all G heads in LDS, K
+// row-major and V transposed, the next block's loads in flight (registers)
+// while the current one is multiplied. Both products run on
 // v_mfma_f32_16x16x32_bf16 in transposed form so no data moves between them:
 //   S^T[key][q] = K[key][:] . Q[q][:]          (A = K rows, B = Q rows)
 //   O^T[d][q]  += V^T[d][keys] . P^T[keys][q]  (B = P^T straight from the
@@ -249,27 +252,31 @@ constexpr int kBlkK = 64;
 constexpr int kKStride = kD + 8;      // K tile row stride (elements): 16-row fragment reads hit distinct banks
 constexpr int kVtStride = kBlkK + 4;  // V^T tile row stride (elements)
 
-template <typename T>
-__global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __restrict__ q,
-                                                           const uint16_t* __restrict__ k,
-                                                           const uint16_t* __restrict__ v, int64_t v_stride,
-                                                           const int32_t* __restrict__ blocks, int Hq, int Hkv,
-                                                           float scale_log2, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[kBlkK * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kVtStride];
+template <typename T, int G>
+__global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* __restrict__ q,
+                                                               const uint16_t* __restrict__ k,
+                                                               const uint16_t* __restrict__ v, int64_t v_stride,
+                                                               const int32_t* __restrict__ blocks, int Hq, int Hkv,
+                                                               float scale_log2, uint16_t* __restrict__ out) {
+  constexpr int kThreads = 256 * G;
+  constexpr int kVec = kBlkK * kD / 8;                 // 16-byte vectors per K (or V) tile
+  constexpr int kPer = kVec / kThreads;                // per thread
+  static_assert(kVec % kThreads == 0, "tile vectors split evenly");
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kBlkK * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kD * kVtStride];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int g = lane >> 4;
   const int r = lane & 15;
-  const int h = blockIdx.y;
-  const int hk = h / (Hq / Hkv);
+  const int h = blockIdx.y * G + (wave >> 2);        // this wave's query head
+  const int hk = h / (Hq / Hkv);                      // the G heads of the workgroup share this kv head
   const int64_t seq0 = blocks[3 * blockIdx.x];      // token offset of the sequence
   const int len = blocks[3 * blockIdx.x + 1];
   const int q0 = blocks[3 * blockIdx.x + 2];         // first query of the block (within the sequence)
 
   // this lane's query (B operand rows of S^T, C columns of both products)
-  const int qi = q0 + wave * 16 + r;
+  const int qi = q0 + (wave & 3) * 16 + r;
   const int qc = min(qi, len - 1);
   u32x4 qf[4];
 #pragma unroll
@@ -281,31 +288,49 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __res
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
 
-  const int kv_end = min(len, q0 + kBlkQ);           // causal: keys < last query of the block + 1
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kBlkK) {
-    __syncthreads();  // previous block's tiles are no longer read
-    {
-      // K tile: thread -> key tid/4, 64-byte quarter tid%4 (coalesced rows)
-      const int key = tid >> 2, part = tid & 3;
-      const int kc = min(kv0 + key, len - 1);
-      const uint16_t* src = k + ((seq0 + kc) * Hkv + hk) * kD + 32 * part;
+  // K/V tile vectors of one key block, held in registers one block ahead.
+  // K vector i -> key i / 16, dims 8 * (i % 16) .. +8 (16 lanes read one
+  // 256-byte row). V vector i -> key i % 64, dims 8 * (i / 64) .. +8, so that
+  // the 64 lanes of a wave write 64 consecutive keys of each V^T row (the
+  // other mapping put 16 lanes on two banks).
+  u32x4 kreg[kPer], vreg[kPer];
+  auto load_tiles = [&](int kv0) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<u32x4*>(&ks[key * kKStride + 32 * part + 8 * j]) =
-            *reinterpret_cast<const u32x4*>(src + 8 * j);
-      // V tile, transposed: thread -> key tid%64, dims 32*(tid/64) .. +32
-      const int vkey = tid & 63, dg = tid >> 6;
-      const int vc = min(kv0 + vkey, len - 1);
-      const uint16_t* vsrc = v + (seq0 + vc) * v_stride + hk * kD + 32 * dg;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(vsrc + 8 * j);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          vt[(32 * dg + 8 * j + e) * kVtStride + vkey] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-      }
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kThreads;
+      const int key = min(kv0 + (i >> 4), len - 1);
+      kreg[j] = *reinterpret_cast<const u32x4*>(k + ((seq0 + key) * Hkv + hk) * kD + 8 * (i & 15));
+      const int vkey = min(kv0 + (i & 63), len - 1);
+      vreg[j] = *reinterpret_cast<const u32x4*>(v + (seq0 + vkey) * v_stride + hk * kD + 8 * (i >> 6));
     }
-    __syncthreads();
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kThreads;
+      *reinterpret_cast<u32x4*>(&ks[buf][(i >> 4) * kKStride + 8 * (i & 15)]) = kreg[j];
+      const int vkey = i & 63, d0 = 8 * (i >> 6);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vt[buf][(d0 + e) * kVtStride + vkey] = (uint16_t)(vreg[j][e >> 1] >> (16 * (e & 1)));
+    }
+  };
+
+  // Pipeline: block b is multiplied from LDS buffer b % 2 while block b+1 is
+  // stored into the other buffer (its global loads were issued one block
+  // earlier) and block b+2 is loaded into registers; one barrier per block.
+  const int kv_end = min(len, q0 + kBlkQ);           // causal: keys < last query of the block + 1
+  load_tiles(0);
+  store_tiles(0);
+  if (kBlkK < kv_end) load_tiles(kBlkK);
+  __syncthreads();
+  for (int kv0 = 0, cur = 0; kv0 < kv_end; kv0 += kBlkK, cur ^= 1) {
+    if (kv0 + kBlkK < kv_end) {
+      store_tiles(cur ^ 1);                               // block + 1 (buffer last read two blocks ago)
+      if (kv0 + 2 * kBlkK < kv_end) load_tiles(kv0 + 2 * kBlkK);
+    }
+    const uint16_t* ksb = ks[cur];
+    const uint16_t* vtb = vt[cur];
 
     // S^T tiles: 4 x (16 keys x 16 queries), k = head dim in 4 chunks of 32
     f32x4 s[4];
@@ -314,7 +339,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __res
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[(kt * 16 + r) * kKStride + 32 * c + 8 * g]);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&ksb[(kt * 16 + r) * kKStride + 32 * c + 8 * g]);
         acc = mfma16x16x32<T>(a, qf[c], acc);
       }
       s[kt] = acc;
@@ -333,13 +358,13 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __res
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
     const float mn = fmaxf(m, mx);  // finite: key 0 is valid for every query
-    const float corr = exp2f(m - mn);
+    const float corr = __builtin_amdgcn_exp2f(m - mn);
     float ps = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const float p = exp2f(s[kt][t] - mn);
+        const float p = __builtin_amdgcn_exp2f(s[kt][t] - mn);
         s[kt][t] = p;
         ps += p;
       }
@@ -362,13 +387,14 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __res
       f32x4 acc = o[dt] * corr;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint16_t* row = &vt[(16 * dt + r) * kVtStride + 32 * c + 4 * g];
+        const uint16_t* row = &vtb[(16 * dt + r) * kVtStride + 32 * c + 4 * g];
         const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
         acc = mfma16x16x32<T>(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c], acc);
       }
       o[dt] = acc;
     }
+    __syncthreads();  // buffer cur is free and buffer cur ^ 1 is complete
   }
 
   if (qi < len) {
@@ -384,22 +410,36 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const uint16_t* __res
   }
 }
 
+template <typename T>
+hipError_t launch_prefill_t(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int64_t v_stride,
+                            const int32_t* blocks, int nblocks, int Hq, int Hkv, float sl2, uint16_t* O,
+                            hipStream_t stream) {
+  // G query heads per workgroup: the largest of 4, 2, 1 dividing the GQA
+  // ratio Hq / Hkv, so the workgroup's heads share one kv head.
+  const int ratio = Hq / Hkv;
+  const int G = ratio % 4 == 0 ? 4 : (ratio % 2 == 0 ? 2 : 1);
+  const dim3 grid((unsigned)nblocks, (unsigned)(Hq / G));
+  if (G == 4)
+    prefill_attn_kernel<T, 4><<<grid, 1024, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O);
+  else if (G == 2)
+    prefill_attn_kernel<T, 2><<<grid, 512, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O);
+  else
+    prefill_attn_kernel<T, 1><<<grid, 256, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_prefill_attention(const void* q, const void* k, const void* v, int64_t v_stride,
                                     const int32_t* blocks, int nblocks, int Hq, int Hkv, float scale, void* out,
                                     bool bf16, hipStream_t stream) {
-  const dim3 grid((unsigned)nblocks, (unsigned)Hq), block(256);
   const float sl2 = scale * 1.4426950408889634f;  // log2(e)
   auto Q = static_cast<const uint16_t*>(q);
   auto Kp = static_cast<const uint16_t*>(k);
   auto V = static_cast<const uint16_t*>(v);
   auto O = static_cast<uint16_t*>(out);
-  if (bf16)
-    prefill_attn_kernel<BF16><<<grid, block, 0, stream>>>(Q, Kp, V, v_stride, blocks, Hq, Hkv, sl2, O);
-  else
-    prefill_attn_kernel<F16><<<grid, block, 0, stream>>>(Q, Kp, V, v_stride, blocks, Hq, Hkv, sl2, O);
-  return hipGetLastError();
+  if (bf16) return launch_prefill_t<BF16>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, stream);
+  return launch_prefill_t<F16>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, stream);
 }
 
 }  // namespace tvq
