@@ -89,7 +89,7 @@ def test_select_path_buckets(hiplib):
     assert sp(_hip.OP_W8A16, 32, 4096, 4096) == "dma_mfma_f16x_32x64"
     assert sp(_hip.OP_W8A8, 17, 6144, 1024) == "dma_mfma_i8_32x64"
     assert sp(_hip.OP_W8A8, 64, 24576, 4096) == "dma_mfma_i8_64x128"     # wide N
-    assert sp(_hip.OP_W8A16, 64, 24576, 4096) == "dma_mfma_f16x_64x128"
+    assert sp(_hip.OP_W8A16, 64, 24576, 4096) == "dma_mfma_f16x_64x128w8"
     assert sp(_hip.OP_W8A8, 16, 24576, 4096) == "dma_mfma_i8_32x64"     # 8 < M <= 16, >= 24 Mi weights
     assert sp(_hip.OP_W8A8, 16, 16384, 1024) == "stream_mfma_i8_m16"    # wide N, smaller weights
     assert sp(_hip.OP_W8A16, 12, 4096, 4096) == "skinny_mfma_f16x_m16"

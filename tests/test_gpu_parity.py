@@ -102,7 +102,7 @@ def test_act_quant_near_ties_bit_exact(hiplib, dtype):
 GEMM_SHAPES = [
     (1, 4096, 1024), (16, 4096, 1024), (17, 1000, 1024), (48, 6144, 1024), (64, 1024, 3072),
     (1, 1024, 12288), (33, 4096, 4096), (7, 200, 2048), (5, 96, 1040), (24, 16384, 512), (64, 16448, 256),
-    (9, 20000, 768), (16, 16384, 1024), (40, 16384, 1024), (64, 24576, 256), (12, 6144, 4096), (16, 4096, 12288),
+    (9, 20000, 768), (16, 16384, 1024), (40, 16384, 1024), (64, 24576, 256), (12, 6144, 4096), (16, 4096, 12288), (48, 16384, 1024),
     (65, 4096, 1024), (256, 4096, 1024), (512, 1024, 3072), (300, 1030, 2048), (129, 136, 80),
     (7, 33, 40), (3, 5, 1024), (2, 4104, 3072), (4, 24576, 4096), (1, 6144, 9216),
 ]
@@ -153,7 +153,7 @@ def test_w8a8_bias(hiplib):
     xq, a_s, q, w_s = _w8a8_inputs(m, n, k, seed=11)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
     d = _dev()
-    for mm in (m, 8):  # tiled and skinny
+    for mm in (m, 8, 2, 1):  # DMA, skinny and GEMV paths
         y = _hip.w8a8_gemm(torch.from_numpy(xq[:mm]).to(d), torch.from_numpy(a_s[:mm]).to(d),
                            torch.from_numpy(q).to(d), torch.from_numpy(w_s).to(d), bias.to(d), torch.bfloat16)
         yb_ref, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq[:mm], q), a_s[:mm], w_s, f32(bias))
@@ -236,7 +236,7 @@ def test_w8a16_bias(hiplib):
     d = _dev()
     q, s = make_weights(520, 1024, seed=3)
     bias = torch.randn(520, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
-    for m in (5, 130):
+    for m in (1, 2, 5, 130):  # GEMV, skinny and DMA paths
         x = make_activations(m, 1024, seed=m, outlier_frac=0.0)
         y = _hip.w8a16_gemm(x.to(d), q.to(d), s.to(d), bias.to(d))
         _w8a16_check(y, x, q, s, bias)
