@@ -41,21 +41,21 @@ enum class DmaCfg {
 // Tile BM x BN, waves WM x WN, ring depth S, MFMA tile MF, per DmaCfg.
 struct CfgInfo {
   bool w8a8;
-  int bm, bn, wm, wn, s, mf;
+  int bm, bn, wm, wn, s, mf, ks;  // ks: k values per ring stage
   const char* name;
   const char* name_split;  // the same tiles with K split over several workgroups
 };
 constexpr CfgInfo kInfo[] = {
-    {true, 256, 256, 2, 4, 2, 32, "dma_mfma_i8_256x256", "dma_mfma_i8_256x256_splitk"},
-    {true, 256, 128, 4, 2, 2, 32, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk"},
-    {true, 64, 64, 2, 2, 4, 16, "dma_mfma_i8_64x64", "dma_mfma_i8_64x64_splitk"},
-    {true, 64, 128, 2, 4, 4, 16, "dma_mfma_i8_64x128", "dma_mfma_i8_64x128_splitk"},
-    {true, 32, 64, 2, 2, 4, 16, "dma_mfma_i8_32x64", "dma_mfma_i8_32x64_splitk"},
-    {false, 128, 256, 2, 4, 2, 32, "dma_mfma_f16x_128x256", "dma_mfma_f16x_128x256_splitk"},
-    {false, 64, 128, 2, 2, 4, 32, "dma_mfma_f16x_64x128", "dma_mfma_f16x_64x128_splitk"},
-    {false, 64, 64, 2, 2, 4, 32, "dma_mfma_f16x_64x64", "dma_mfma_f16x_64x64_splitk"},
-    {false, 32, 64, 2, 2, 4, 16, "dma_mfma_f16x_32x64", "dma_mfma_f16x_32x64_splitk"},
-    {false, 64, 128, 2, 4, 4, 16, "dma_mfma_f16x_64x128w8", "dma_mfma_f16x_64x128w8_splitk"},
+    {true, 256, 256, 2, 4, 2, 32, 128, "dma_mfma_i8_256x256", "dma_mfma_i8_256x256_splitk"},
+    {true, 256, 128, 4, 2, 2, 32, 128, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk"},
+    {true, 64, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_64x64", "dma_mfma_i8_64x64_splitk"},
+    {true, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_i8_64x128", "dma_mfma_i8_64x128_splitk"},
+    {true, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_32x64", "dma_mfma_i8_32x64_splitk"},
+    {false, 128, 256, 2, 4, 2, 32, 128, "dma_mfma_f16x_128x256", "dma_mfma_f16x_128x256_splitk"},
+    {false, 64, 128, 2, 2, 4, 32, 128, "dma_mfma_f16x_64x128", "dma_mfma_f16x_64x128_splitk"},
+    {false, 64, 64, 2, 2, 4, 32, 128, "dma_mfma_f16x_64x64", "dma_mfma_f16x_64x64_splitk"},
+    {false, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_f16x_32x64", "dma_mfma_f16x_32x64_splitk"},
+    {false, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_f16x_64x128w8", "dma_mfma_f16x_64x128w8_splitk"},
 };
 
 static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_64x128w8 + 1, "one entry per DmaCfg");
@@ -113,7 +113,7 @@ int splits_of(int64_t M, int64_t N, int64_t K, const void* ws, int64_t ws_bytes)
   } else {
     if (!split_shape(M, N, K)) return 1;
     constexpr CfgInfo i = info<c>();
-    return dma::choose_splits((int)tiles(M, N, i.bm, i.bn), (int)(K / 128), dma::device_cus(), i.bm * i.bn * 4, ws,
+    return dma::choose_splits((int)tiles(M, N, i.bm, i.bn), (int)(K / i.ks), dma::device_cus(), i.bm * i.bn * 4, ws,
                               ws_bytes);
   }
 }
@@ -137,11 +137,11 @@ hipError_t go(const GemmArgs& a, hipStream_t s) {
   // registers; measured ~4 % faster on the M=256 headline shape).
   if constexpr (splittable<c>()) {
     if (splits > 1)
-      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, true>(
+      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, true>(
           a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), splits,
           a.workspace, a.workspace_bytes, s);
   }
-  return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, false>(
+  return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false>(
       a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0,
       s);
 }

@@ -1,8 +1,10 @@
 // Multi-stage LDS-DMA pipelined W8A16 / W8A8 GEMM for gfx950 (kernel template).
 //
 // Operands are moved global -> LDS with global_load_lds_dwordx4 (no register
-// staging) into an S-deep ring of stages; each stage covers 128 k values, so
-// S-1 stages of loads are in flight while the MFMAs of the current one run.
+// staging) into an S-deep ring of stages; each stage covers KS = 128 (or 64)
+// k values, so S-1 stages of loads are in flight while the MFMAs of the
+// current one run. Each wave's DMA ops for a stage go out in two halves,
+// one sub-step apart.
 //
 // One wave-level DMA fills one 1 KB block: 8 rows x 128 contiguous bytes of
 // the operand (full cache lines). Lane i fetches row rho = i/8 of the block,
@@ -13,7 +15,8 @@
 // of equal parity land 256 bytes apart, and swz gives the 8 rows of each
 // parity in a 16-row group 8 different chunk slots, so the 16 lanes of a
 // fragment read (16 rows, one logical chunk) never share a bank, while every
-// DMA still reads whole 128-byte lines.
+// DMA still reads whole 128-byte lines. (With KS = 64 a block holds 16 rows
+// x 64 bytes and the same reasoning gives swz(row) = (row/4) % 4.)
 //
 // Fragment reads (one ds_read_b128 per lane, lane = 16*g + r):
 //   weight / int8 activation, 64-k sub-step ks: row r, chunk 4*ks + g
@@ -33,7 +36,11 @@
 //
 // Waits are explicit: the compiler does not track LDS-DMA completion, so each
 // step waits on vmcnt for its own stage and then crosses an s_barrier (a bare
-// barrier, without the workgroup fence that would force vmcnt(0)).
+// barrier, without the workgroup fence that would force vmcnt(0)). The
+// fragments of each sub-step are read from LDS one sub-step ahead into a
+// second register set, and the crossing into the next stage happens before
+// the MFMAs of a stage's last sub-step, so the matrix core always has queued
+// work while a wave waits.
 //
 // The grid is persistent when there are more tiles than resident workgroups:
 // each workgroup walks tiles blockIdx.x, +gridDim.x, ... After the last
@@ -75,6 +82,10 @@ __device__ __forceinline__ void wait_vm() {
 
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// s_waitcnt immediate for lgkmcnt(0) with vmcnt and expcnt left at their
+// maxima (gfx9 encoding: vmcnt 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int kWaitLgkm0 = 0xC07F;
+
 // Wait until at most `ahead` later stages (each `LPW` DMA ops) are in flight
 // (0 <= ahead <= S-2); vmcnt retires in issue order.
 template <int LPW, int S, int A = S - 2>
@@ -96,18 +107,20 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 constexpr int64_t kSplitCntBytes = 64 * 1024;
 constexpr int kSplitMaxTiles = (int)(kSplitCntBytes / 4);
 
-template <bool kW8A8, int BM, int BN, int WM, int WN, int S, int MF>
+template <bool kW8A8, int BM, int BN, int WM, int WN, int S, int MF, int KS>
 struct Cfg {
   static constexpr int kThreads = 64 * WM * WN;
   static constexpr int kWaves = WM * WN;
-  static constexpr int kXHalves = kW8A8 ? 1 : 2;          // 128-byte segments per activation row per stage
-  static constexpr int kWBlk = BN / 8;                    // weight blocks per stage
-  static constexpr int kXBlk = (BM / 8) * kXHalves;       // activation blocks per stage
+  static constexpr int kXRow = kW8A8 ? KS : 2 * KS;      // activation bytes per row per stage
+  static constexpr int kXRb = kXRow < 128 ? kXRow : 128;  // activation block row width
+  static constexpr int kXHalves = kXRow / kXRb;           // activation blocks per row group per stage
+  static constexpr int kWBlk = BN * KS / 1024;            // weight blocks per stage
+  static constexpr int kXBlk = BM * kXRow / 1024;         // activation blocks per stage
   static constexpr int kBlkStage = kWBlk + kXBlk;
   static constexpr int kStageBytes = kBlkStage * 1024;
   static constexpr int kRingBytes = kStageBytes * S;
   static constexpr int kLPW = kBlkStage / kWaves;         // DMA ops per wave per stage
-  static constexpr int kKStage = 128;                     // k values per stage
+  static constexpr int kKStage = KS;                      // k values per stage
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / MF, FN = TN / MF;        // MFMA tiles per wave
   static constexpr int kEpiBytes = MF * TN * 2;           // per-wave staging: MF rows x TN 16-bit outputs
@@ -117,6 +130,7 @@ struct Cfg {
   static_assert(kBlkStage % kWaves == 0, "stage blocks must split evenly over waves");
   static_assert(TM % MF == 0 && TN % MF == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(S >= 2, "at least double buffering");
+  static_assert(KS == 64 || KS == 128, "stage depth is 64 or 128 k");
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
   static_assert(kWaves * kEpiBytes <= kStageBytes, "epilogue staging must fit in one ring stage");
 };
@@ -163,10 +177,17 @@ __device__ __forceinline__ void store4(void* yv, const float* ws, const uint16_t
 
 // Offset (bytes) of 16-byte chunk `c` of row `row` inside a run of 8-row
 // blocks laid out by the DMA (chunk c of row rho at slot rho*8 + (c ^ swz)).
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+// For 64-byte rows (16-row blocks, 4 chunks per row) the same rule reads: chunk c
+// of row rho at slot rho*4 + (c ^ swz(row)), swz(row) = (row/4) % 4.
+template <int RB>
+__device__ __forceinline__ int swz(int row) {
+  return RB == 128 ? (row >> 1) & 7 : (row >> 2) & 3;
+}
 
+template <int RB>
 __device__ __forceinline__ int chunk_off(int row, int c) {
-  return (row >> 3) * 1024 + 16 * ((row & 7) * 8 + (c ^ swz(row)));
+  constexpr int kR = 1024 / RB, kC = RB / 16;  // rows per block, chunks per row
+  return (row / kR) * 1024 + 16 * ((row % kR) * kC + (c ^ swz<RB>(row)));
 }
 
 // Tile order: XCD chunking (workgroup i runs on XCD i % 8, so each XCD gets a
@@ -195,7 +216,7 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
   }
 }
 
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, bool kSplit>
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
@@ -204,7 +225,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
                                                                 void* __restrict__ yv, int M, int N, int K,
                                                                 int group, int m_major, int splits,
                                                                 char* __restrict__ wsp) {
-  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
+  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
   using Acc = typename std::conditional<
       MF == 32, typename std::conditional<kW8A8, i32x16, f32x16>::type,
       typename std::conditional<kW8A8, i32x4, f32x4>::type>::type;
@@ -237,7 +258,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   const char* wbase = reinterpret_cast<const char*>(qw);
   const char* xbase = static_cast<const char*>(xv);
   int soff[C::kLPW];
-  const int drho = lane >> 3;             // row within the 8-row block
+  constexpr int kWCh = KS / 16, kXCh = C::kXRb / 16;   // 16-byte chunks per block row
   auto set_sources = [&](int m0, int n0, int kb) {
     wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K + (int64_t)kb * C::kKStage;
     xbase = static_cast<const char*>(xv) + ((int64_t)m0 * K + (int64_t)kb * C::kKStage) * (kW8A8 ? 1 : 2);
@@ -245,34 +266,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     for (int j = 0; j < C::kLPW; ++j) {
       const int b = j * C::kWaves + wave;
       if (b < C::kWBlk) {
-        const int row = 8 * b + drho;                       // row of the tile's weight panel
+        const int row = (1024 / KS) * b + lane / kWCh;      // row of the tile's weight panel
         const int n = min(n0 + row, N - 1) - n0;
-        soff[j] = n * K + 16 * ((lane & 7) ^ swz(row));
+        soff[j] = n * K + 16 * ((lane % kWCh) ^ swz<KS>(row));
       } else {
         const int xb = b - C::kWBlk;
-        const int row = 8 * (xb / C::kXHalves) + drho;      // row of the tile's activation panel
+        const int row = (1024 / C::kXRb) * (xb / C::kXHalves) + lane / kXCh;  // row of the activation panel
         const int m = min(m0 + row, M - 1) - m0;
         const int half = xb % C::kXHalves;
-        soff[j] = m * K * (kW8A8 ? 1 : 2) + 128 * half + 16 * ((lane & 7) ^ swz(row));
+        soff[j] = m * K * (kW8A8 ? 1 : 2) + C::kXRb * half + 16 * ((lane % kXCh) ^ swz<C::kXRb>(row));
       }
     }
   };
-  auto issue = [&](int kt) {
+  auto issue = [&](int kt, int j0 = 0, int j1 = C::kLPW) {
     char* stage = smem + (kt % S) * C::kStageBytes;
 #pragma unroll
     for (int j = 0; j < C::kLPW; ++j) {
+      if (j < j0 || j >= j1) continue;
       const int b = j * C::kWaves + wave;
       const bool wblk = b < C::kWBlk;
-      const int step = (wblk || kW8A8) ? C::kKStage : 2 * C::kKStage;
+      const int step = wblk ? KS : C::kXRow;
       const char* p = (wblk ? wbase : xbase) + soff[j] + (int64_t)kt * step;
       __builtin_amdgcn_global_load_lds(TVQ_GPTR(p), TVQ_LPTR(stage + b * 1024), 16, 0, 0);
     }
   };
 
   // ---- lane-constant fragment offsets within a stage ---------------------
-  // MF = 16: lane = 16*g + r, sub-steps of 64 k (2 per stage).
-  // MF = 32: lane = 32*h + r, sub-steps of 32 k (4 per stage).
-  constexpr int kSub = MF == 32 ? 4 : 2;
+  // MF = 16: lane = 16*g + r, sub-steps of 64 k (KS / 64 per stage).
+  // MF = 32: lane = 32*h + r, sub-steps of 32 k (KS / 32 per stage).
+  constexpr int kSub = KS / (MF == 32 ? 32 : 64);
   constexpr int kRows = MF;                        // rows per fragment
   const int r = lane % MF;
   const int g = lane / MF;                         // lane group: 0..3 (MF 16) or 0..1 (MF 32)
@@ -280,21 +302,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   int xoff[kSub][2];     // 16-bit activation fragment, halves b = 0, 1
 #pragma unroll
   for (int ks = 0; ks < kSub; ++ks) {
-    // 16 bytes per lane: k = ks*(128/kSub) + 16*g .. +16
-    const int c = ks * (8 / kSub) + g;
-    woff[ks] = chunk_off(r, c);
+    // 16 bytes per lane: k = ks*(KS/kSub) + 16*g .. +16
+    const int c = ks * (kWCh / kSub) + g;
+    woff[ks] = chunk_off<KS>(r, c);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      // 16-bit activations: k = ks*(128/kSub) + 16*g + 8*b .. +8, two 64-k halves per row
-      const int k = ks * (128 / kSub) + 16 * g + 8 * b;
-      const int rho = r & 7;
-      xoff[ks][b] = (r >> 3) * 2048 + (k >> 6) * 1024 + 16 * (rho * 8 + (((k & 63) >> 3) ^ swz(r)));
+      // 16-bit activations: k = ks*(KS/kSub) + 16*g + 8*b .. +8, one 128-byte
+      // block (64 k) per half of the row
+      const int k = ks * (KS / kSub) + 16 * g + 8 * b;
+      xoff[ks][b] = (r >> 3) * 1024 * C::kXHalves + (k >> 6) * 1024 + 16 * ((r & 7) * 8 + (((k & 63) >> 3) ^ swz<128>(r)));
     }
   }
-  constexpr int kWFrag = kRows / 8 * 1024;         // bytes per weight fragment (rows x 128 B)
-  constexpr int kXFrag = kW8A8 ? kWFrag : 2 * kWFrag;
+  constexpr int kWFrag = kRows * KS;               // bytes per weight fragment (rows x KS bytes)
+  constexpr int kXFrag = kRows * C::kXRow;
   constexpr int kReadsPerSub = C::FN + C::FM * (kW8A8 ? 1 : 2);   // ds_read_b128 per sub-step
   constexpr int kMfmaPerSub = C::FN * C::FM * (kW8A8 ? 1 : 2);    // MFMAs per sub-step
+  static_assert(kSub % 2 == 0, "fragment buffers alternate per sub-step across stages");
 
   // ---- per-tile scales and bias, parked in LDS for the epilogue ----------
   float* sc = reinterpret_cast<float*>(smem + C::kRingBytes);  // [a_s: BM | w_s: BN | bias: BN]
@@ -342,40 +365,64 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 #pragma unroll
       for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
 
-    for (int kt = 0; kt < cur_nk; ++kt) {
-      wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 1 - kt));
-      barrier();
-      if constexpr (!kRaw) {
-        // after the barrier: the previous tile's epilogue no longer reads them
-        if (kt == 0) store_scales();
-      }
-      if (kt + S - 1 < cur_nk) issue(kt + S - 1);
-
+    // Fragments are double-buffered in registers: the LDS reads of sub-step
+    // ks+1 are issued among the MFMAs of sub-step ks, so their latency hides
+    // behind the matrix core instead of stalling the wave. The stage boundary
+    // is crossed one sub-step early: before the MFMAs of a stage's last
+    // sub-step the waves wait for the next stage's DMA, meet at the barrier,
+    // refill the ring and read the next stage's first fragments, so the
+    // pipeline never drains at a barrier.
+    u32x4 fa[2][C::FN];
+    u32x4 fb[2][C::FM][kW8A8 ? 1 : 2];
+    auto load_frags = [&](int kt, int ks, int buf) {
       const char* wst = smem + (kt % S) * C::kStageBytes + wn * C::FN * kWFrag;
       const char* xst = smem + (kt % S) * C::kStageBytes + C::kWBlk * 1024 + wm * C::FM * kXFrag;
-      // Fragments are double-buffered in registers: the LDS reads of sub-step
-      // ks+1 are issued among the MFMAs of sub-step ks, so their latency hides
-      // behind the matrix core instead of stalling the wave.
-      u32x4 fa[2][C::FN];
-      u32x4 fb[2][C::FM][kW8A8 ? 1 : 2];
-      auto load_frags = [&](int ks, int buf) {
 #pragma unroll
-        for (int i = 0; i < C::FN; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(wst + i * kWFrag + woff[ks]);
+      for (int i = 0; i < C::FN; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(wst + i * kWFrag + woff[ks]);
 #pragma unroll
-        for (int j = 0; j < C::FM; ++j) {
-          if constexpr (kW8A8) {
-            fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + woff[ks]);
-          } else {
-            fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][0]);
-            fb[buf][j][1] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][1]);
-          }
+      for (int j = 0; j < C::FM; ++j) {
+        if constexpr (kW8A8) {
+          fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + woff[ks]);
+        } else {
+          fb[buf][j][0] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][0]);
+          fb[buf][j][1] = *reinterpret_cast<const u32x4*>(xst + j * kXFrag + xoff[ks][1]);
         }
-      };
-      load_frags(0, 0);
+      }
+    };
+
+    wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 1));
+    barrier();
+    // after the barrier: the previous tile's epilogue no longer reads them
+    if constexpr (!kRaw) store_scales();
+    if (S - 1 < cur_nk) issue(S - 1);
+    load_frags(0, 0, 0);
+
+    for (int kt = 0; kt < cur_nk; ++kt) {
 #pragma unroll
       for (int ks = 0; ks < kSub; ++ks) {
         const int cb = ks & 1;
-        if (ks + 1 < kSub) load_frags(ks + 1, cb ^ 1);
+        // This sub-step's fragments were requested one sub-step ago. The
+        // wait is the s_waitcnt builtin (not inline asm) so the compiler
+        // knows every earlier LDS read is complete and adds no wait of its
+        // own after the reads issued next.
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Second half of the DMA ops for stage kt - 1 + S (the first half
+        // went out at the previous stage crossing): spreading a stage's
+        // loads over two sub-steps keeps the waves from stalling behind a
+        // burst of vector-memory issues while the matrix core idles.
+        if (ks == 0 && kt > 0 && kt - 1 + S < cur_nk) issue(kt - 1 + S, C::kLPW / 2, C::kLPW);
+        if (ks + 1 < kSub) {
+          load_frags(kt, ks + 1, cb ^ 1);
+        } else if (kt + 1 < cur_nk) {
+          // Every wave's reads of stage kt are complete (the wait above);
+          // once all are past the barrier the slot of stage kt can take
+          // stage kt + S.
+          wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 2 - kt));
+          barrier();
+          if (kt + S < cur_nk) issue(kt + S, 0, C::kLPW / 2);
+          load_frags(kt + 1, 0, cb ^ 1);
+        }
         if constexpr (kW8A8) {
 #pragma unroll
           for (int j = 0; j < C::FM; ++j) {
@@ -408,15 +455,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
             }
           }
         }
-        // Interleave the next sub-step's LDS reads with this sub-step's MFMAs
-        // (one read, then its share of MFMAs), so the LDS port and the matrix
-        // core work in parallel instead of in bursts.
+        // All of the next fragments' reads go out ahead of this sub-step's
+        // MFMAs (otherwise the scheduler sinks them below the MFMAs that
+        // last read the registers it would reuse, exposing their latency).
         if (ks + 1 < kSub) {
-#pragma unroll
-          for (int rr = 0; rr < kReadsPerSub; ++rr) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, (kMfmaPerSub + kReadsPerSub - 1) / kReadsPerSub, 0);
-          }
+          __builtin_amdgcn_sched_group_barrier(0x100, kReadsPerSub, 0);  // DS reads
+          __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerSub, 0);   // MFMAs
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -624,12 +668,12 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
   return (nk + per - 1) / per;
 }
 
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, bool kSplit>
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
                       int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
                       hipStream_t stream) {
-  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF>;
-  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, kSplit>;
+  using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
