@@ -577,56 +577,74 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       const float* sc_b = sc + BM + BN + wn * C::TN;
       uint16_t* y = static_cast<uint16_t*>(yv);
       const bool vec = (N & 7) == 0;
+      // Per-channel scales of this lane's columns, read once for all row
+      // slices (LDS reads of the scales were a large share of the epilogue);
+      // the bias, when there is one, is read per use.
+      f32x4 wsv[C::FN][kQ];
 #pragma unroll
-      for (int j = 0; j < C::FM; ++j) {
-        const int mrow0 = m0 + wm * C::TM + MF * j;  // first output row of this slice
-        float as = 0.0f;
-        if constexpr (kW8A8) as = sc[wm * C::TM + MF * j + r];
+      for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-        for (int i = 0; i < C::FN; ++i) {
+        for (int q = 0; q < kQ; ++q) wsv[i][q] = *reinterpret_cast<const f32x4*>(sc_w + MF * i + 8 * q + 4 * g);
+      const bool has_bias = bias != nullptr;
+      auto epi_slices = [&](auto bias_c) {
+        constexpr bool kBias = decltype(bias_c)::value;
 #pragma unroll
-          for (int q = 0; q < kQ; ++q) {
-            const int nl = MF * i + 8 * q + 4 * g;   // column within the wave tile (multiple of 4)
-            const f32x4 wv = *reinterpret_cast<const f32x4*>(sc_w + nl);
-            const f32x4 bv = *reinterpret_cast<const f32x4*>(sc_b + nl);
-            float o[4];
+        for (int j = 0; j < C::FM; ++j) {
+          const int mrow0 = m0 + wm * C::TM + MF * j;  // first output row of this slice
+          float as = 0.0f;
+          if constexpr (kW8A8) as = sc[wm * C::TM + MF * j + r];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              if constexpr (kW8A8)
-                o[t] = epi_w8a8(acc[i][j][4 * q + t], as, wv[t], bv[t]);
-              else
-                o[t] = epi_w8a16(acc[i][j][4 * q + t], wv[t], bv[t]);
-            }
-            u32x2 pk;
-            pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
-            pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
-            *reinterpret_cast<u32x2*>(stg + r * kRowB + 16 * ((nl >> 3) ^ sswz(r)) + 2 * (nl & 7)) = pk;
-          }
-        }
-        // LDS operations of one wave complete in order; the wait and the
-        // compiler barrier keep the read-back after the writes above.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          for (int i = 0; i < C::FN; ++i) {
 #pragma unroll
-        for (int ps = 0; ps < kPass; ++ps) {
-          const int e = ps * 64 + lane;
-          const int row = e / kCh;
-          const int ch = e % kCh;
-          const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kRowB + 16 * (ch ^ sswz(row)));
-          const int mo = mrow0 + row;
-          const int no = ncol0 + 8 * ch;
-          if (mo < M && no < N) {
-            uint16_t* dst = y + (int64_t)mo * N + no;
-            if (vec && no + 8 <= N) {
-              *reinterpret_cast<u32x4*>(dst) = val;
-            } else {
+            for (int q = 0; q < kQ; ++q) {
+              const int nl = MF * i + 8 * q + 4 * g;   // column within the wave tile (multiple of 4)
+              f32x4 bv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+              if constexpr (kBias) bv = *reinterpret_cast<const f32x4*>(sc_b + nl);
+              float o[4];
 #pragma unroll
-              for (int t = 0; t < 8; ++t)
-                if (no + t < N) dst[t] = (uint16_t)(val[t >> 1] >> (16 * (t & 1)));
+              for (int t = 0; t < 4; ++t) {
+                if constexpr (kW8A8)
+                  o[t] = kBias ? epi_w8a8(acc[i][j][4 * q + t], as, wsv[i][q][t], bv[t])
+                               : epi_w8a8_nb(acc[i][j][4 * q + t], as, wsv[i][q][t]);
+                else
+                  o[t] = kBias ? epi_w8a16(acc[i][j][4 * q + t], wsv[i][q][t], bv[t])
+                               : epi_w8a16_nb(acc[i][j][4 * q + t], wsv[i][q][t]);
+              }
+              u32x2 pk;
+              pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
+              pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
+              *reinterpret_cast<u32x2*>(stg + r * kRowB + 16 * ((nl >> 3) ^ sswz(r)) + 2 * (nl & 7)) = pk;
             }
           }
+          // LDS operations of one wave complete in order; the wait and the
+          // compiler barrier keep the read-back after the writes above.
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int ps = 0; ps < kPass; ++ps) {
+            const int e = ps * 64 + lane;
+            const int row = e / kCh;
+            const int ch = e % kCh;
+            const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kRowB + 16 * (ch ^ sswz(row)));
+            const int mo = mrow0 + row;
+            const int no = ncol0 + 8 * ch;
+            if (mo < M && no < N) {
+              uint16_t* dst = y + (int64_t)mo * N + no;
+              if (vec && no + 8 <= N) {
+                *reinterpret_cast<u32x4*>(dst) = val;
+              } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                  if (no + t < N) dst[t] = (uint16_t)(val[t >> 1] >> (16 * (t & 1)));
+              }
+            }
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      }
+      };
+      if (has_bias)
+        epi_slices(std::true_type{});
+      else
+        epi_slices(std::false_type{});
     }
     if (!more) break;
   }

@@ -138,6 +138,12 @@ __device__ __forceinline__ float epi_w8a16(float acc, float s, float b) { return
 __device__ __forceinline__ float epi_w8a8(int32_t acc, float as, float ws, float b) {
   return __builtin_fmaf((float)acc * as, ws, b);
 }
+// The same with no bias tensor: b = +0 (an fma with +0, not a plain
+// multiply, so that a -0 product still rounds to +0 exactly as above).
+__device__ __forceinline__ float epi_w8a8_nb(int32_t acc, float as, float ws) {
+  return __builtin_fmaf((float)acc * as, ws, 0.0f);
+}
+__device__ __forceinline__ float epi_w8a16_nb(float acc, float s) { return __builtin_fmaf(acc, s, 0.0f); }
 
 // Per-token int8 code of x for scale s, bit-identical to
 // clamp(rint(x / s), -127, 127) with an IEEE round-to-nearest divide
