@@ -247,10 +247,13 @@ hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* 
 // product (as flash attention does).
 namespace {
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+#define TVQ_LDS_V4I16(p) ((__attribute__((address_space(3))) v4i16*)(p))
+
 constexpr int kBlkQ = 64;
 constexpr int kBlkK = 64;
 constexpr int kKStride = kD + 8;      // K tile row stride (elements): 16-row fragment reads hit distinct banks
-constexpr int kVtStride = kBlkK + 4;  // V^T tile row stride (elements)
+constexpr int kVStride = kD + 16;     // V tile row stride (elements): the 4 rows of a transposing read hit distinct banks
 
 template <typename T, int G>
 __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* __restrict__ q,
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
   constexpr int kPer = kVec / kThreads;                // per thread
   static_assert(kVec % kThreads == 0, "tile vectors split evenly");
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][kBlkK * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kD * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kBlkK * kVStride];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -289,10 +292,8 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
   float m = -INFINITY, l = 0.0f;
 
   // K/V tile vectors of one key block, held in registers one block ahead.
-  // K vector i -> key i / 16, dims 8 * (i % 16) .. +8 (16 lanes read one
-  // 256-byte row). V vector i -> key i % 64, dims 8 * (i / 64) .. +8, so that
-  // the 64 lanes of a wave write 64 consecutive keys of each V^T row (the
-  // other mapping put 16 lanes on two banks).
+  // Vector i -> key i / 16, dims 8 * (i % 16) .. +8 (16 lanes read one
+  // 256-byte row), for K and V alike; both tiles stay row-major in LDS.
   u32x4 kreg[kPer], vreg[kPer];
   auto load_tiles = [&](int kv0) {
 #pragma unroll
@@ -300,8 +301,7 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
       const int i = tid + j * kThreads;
       const int key = min(kv0 + (i >> 4), len - 1);
       kreg[j] = *reinterpret_cast<const u32x4*>(k + ((seq0 + key) * Hkv + hk) * kD + 8 * (i & 15));
-      const int vkey = min(kv0 + (i & 63), len - 1);
-      vreg[j] = *reinterpret_cast<const u32x4*>(v + (seq0 + vkey) * v_stride + hk * kD + 8 * (i >> 6));
+      vreg[j] = *reinterpret_cast<const u32x4*>(v + (seq0 + key) * v_stride + hk * kD + 8 * (i & 15));
     }
   };
   auto store_tiles = [&](int buf) {
@@ -309,10 +309,7 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
     for (int j = 0; j < kPer; ++j) {
       const int i = tid + j * kThreads;
       *reinterpret_cast<u32x4*>(&ks[buf][(i >> 4) * kKStride + 8 * (i & 15)]) = kreg[j];
-      const int vkey = i & 63, d0 = 8 * (i >> 6);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        vt[buf][(d0 + e) * kVtStride + vkey] = (uint16_t)(vreg[j][e >> 1] >> (16 * (e & 1)));
+      *reinterpret_cast<u32x4*>(&vs[buf][(i >> 4) * kVStride + 8 * (i & 15)]) = vreg[j];
     }
   };
 
@@ -330,7 +327,7 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
       if (kv0 + 2 * kBlkK < kv_end) load_tiles(kv0 + 2 * kBlkK);
     }
     const uint16_t* ksb = ks[cur];
-    const uint16_t* vtb = vt[cur];
+    const uint16_t* vsb = vs[cur];
 
     // S^T tiles: 4 x (16 keys x 16 queries), k = head dim in 4 chunks of 32
     f32x4 s[4];
@@ -381,15 +378,24 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
       pb[c][2] = (uint32_t)from_float<T>(s[2 * c + 1][0]) | ((uint32_t)from_float<T>(s[2 * c + 1][1]) << 16);
       pb[c][3] = (uint32_t)from_float<T>(s[2 * c + 1][2]) | ((uint32_t)from_float<T>(s[2 * c + 1][3]) << 16);
     }
-    // O^T tiles: 8 x (16 dims x 16 queries), k = 64 keys in 2 chunks
+    // O^T tiles: 8 x (16 dims x 16 queries), k = 64 keys in 2 chunks. The
+    // A operand V^T[d][keys] comes from the row-major V tile through the
+    // LDS transposing read (ds_read_b64_tr_b16): within each 16-lane group,
+    // result element e of lane i is element i % 4 of the 4-element row
+    // addressed by lane 4e + i / 4. Lane (g, r) therefore addresses key
+    // 4g + r / 4 (+ 32c, + 16 for the high half), dims 16dt + 4(r % 4) .. +4,
+    // and receives V[32c + 4g + e][16dt + r], e = 0..3: row d = 16dt + r of
+    // V^T at the keys its P^T chunk holds.
+    const uint16_t* vrow = vsb + (4 * g + (r >> 2)) * kVStride + 4 * (r & 3);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       f32x4 acc = o[dt] * corr;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint16_t* row = &vtb[(16 * dt + r) * kVtStride + 32 * c + 4 * g];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+        const uint16_t* p0 = vrow + 32 * c * kVStride + 16 * dt;
+        const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(TVQ_LDS_V4I16(p0)));
+        const u32x2 hi =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(TVQ_LDS_V4I16(p0 + 16 * kVStride)));
         acc = mfma16x16x32<T>(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c], acc);
       }
       o[dt] = acc;
