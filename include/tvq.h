@@ -210,13 +210,17 @@ int tvq_qk_norm_rope(const void* qkv, int64_t row_stride,
                      const int64_t* slots, int64_t num_slots, int64_t max_len,
                      int dtype, void* stream);
 
+/* Queries per row of the tvq_prefill_attention block table. */
+#define TVQ_PREFILL_BLOCK_Q 64
+
 /* Causal attention over the packed prompts of a prefill step (no cached
  * prefix). Replaces flash_attn_varlen_func(q, k, v, cu_seqlens..., causal=True)
  * in the prefill branch of Attention.forward (nanovllm/layers/attention.py:75-84).
  *   q [T, Hq, head_dim], k [T, Hkv, head_dim]   contiguous, packed tokens
  *   v [T, ...]  row stride v_stride elements, heads contiguous (head_dim each)
  *   blocks [nblocks, 3] int32: (token offset of the sequence, its length,
- *          first query of a 64-query block), one row per query block
+ *          first query of a TVQ_PREFILL_BLOCK_Q-query block), one row per
+ *          query block
  *   out [T, Hq, head_dim] contiguous
  * out[t, h] = softmax(scale * q[t,h] . K_seq[0..pos]) V_seq[0..pos] over the
  * sequence's own keys up to its position (kv head h / (Hq/Hkv)). fp32 math;

@@ -237,3 +237,14 @@ def test_utils_quantizers_match_oracle():
     assert torch.equal(q2, q) and torch.equal(s2, s)
     assert is_qwen3_int8_target_weight("model.layers.0.mlp.down_proj.weight")
     assert not is_qwen3_int8_target_weight("model.layers.0.input_layernorm.weight")
+
+
+def test_prefill_block_size_matches_header():
+    """The host block table and the kernel agree on the query block size."""
+    import re
+    from pathlib import Path
+    from nanovllm.quantization import _hip
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "tvq.h").read_text()
+    assert int(re.search(r"#define TVQ_PREFILL_BLOCK_Q (\d+)", hdr).group(1)) == _hip.PREFILL_BLOCK_Q
+    rows = _hip.prefill_blocks([(0, 130), (130, 64)]).tolist()
+    assert sorted(r[2] for r in rows if r[0] == 0) == list(range(0, 130, _hip.PREFILL_BLOCK_Q))

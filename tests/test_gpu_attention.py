@@ -122,7 +122,7 @@ def _prefill_ref(q, k, v, lens, scale):
 def test_prefill_attention_matches_fp32_reference(hiplib, hq, hkv, dtype):
     from nanovllm.quantization import _hip
     print(f"CASE prefill_attention hq={hq} hkv={hkv} dtype={dtype}", flush=True)
-    lens = [1, 5, 64, 65, 100, 300, 1024, 17]
+    lens = [1, 5, 64, 65, 100, 300, 1024, 17, 128, 129, 255]
     t, d = sum(lens), 128
     g = torch.Generator(device="cuda").manual_seed(hq + hkv)
     q = torch.randn(t, hq, d, device="cuda", generator=g).to(dtype)

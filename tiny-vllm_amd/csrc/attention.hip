@@ -26,6 +26,7 @@
 // read once (2 * len * D * 2 bytes per kv head).
 #include "tvq_common.h"
 #include "tvq_internal.h"
+#include "../../include/tvq.h"
 
 namespace tvq {
 namespace {
@@ -250,7 +251,7 @@ namespace {
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 #define TVQ_LDS_V4I16(p) ((__attribute__((address_space(3))) v4i16*)(p))
 
-constexpr int kBlkQ = 64;
+constexpr int kBlkQ = TVQ_PREFILL_BLOCK_Q;  // queries per block: 4 waves x 16
 constexpr int kBlkK = 64;
 constexpr int kKStride = kD + 8;      // K tile row stride (elements): 16-row fragment reads hit distinct banks
 constexpr int kVStride = kD + 16;     // V tile row stride (elements): the 4 rows of a transposing read hit distinct banks

@@ -411,10 +411,13 @@ def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, 
     return q, k
 
 
-def prefill_blocks(offsets_lens: list[tuple[int, int]], block_q: int = 64) -> torch.Tensor:
+PREFILL_BLOCK_Q = 64  # TVQ_PREFILL_BLOCK_Q in include/tvq.h
+
+
+def prefill_blocks(offsets_lens: list[tuple[int, int]], block_q: int = PREFILL_BLOCK_Q) -> torch.Tensor:
     """Host-side block table for prefill_attention: one (token offset,
-    length, first query) row per 64-query block, blocks with the most keys
-    first (they take longest)."""
+    length, first query) row per PREFILL_BLOCK_Q-query block, blocks with the
+    most keys first (they take longest)."""
     rows = [(off, n, q0) for off, n in offsets_lens for q0 in range(0, n, block_q)]
     rows.sort(key=lambda x: -x[2])
     return torch.tensor(rows, dtype=torch.int32).reshape(-1, 3)
