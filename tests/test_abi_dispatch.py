@@ -96,7 +96,8 @@ def test_select_path_buckets(hiplib):
     assert sp(_hip.OP_W8A8, 64, 6144, 1040) == "skinny_mfma_i8_m64"     # K % 128 != 0 keeps skinny
     assert sp(_hip.OP_W8A8, 8, 24576, 4096) == "skinny_mfma_i8_m16"     # M <= 8
     assert sp(_hip.OP_W8A8, 16, 24576, 4160) == "skinny_mfma_i8_m16"    # K % 256 != 0
-    assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_32x64"
+    assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_64x64"     # 64x64 tiles fill the CUs
+    assert sp(_hip.OP_W8A8, 192, 4096, 1024) == "dma_mfma_i8_32x64"
     assert sp(_hip.OP_W8A8, 8192, 1024, 3072) == "dma_mfma_i8_256x128"
     assert sp(_hip.OP_W8A8, 8192, 6144, 1024) == "dma_mfma_i8_256x256"
     assert sp(_hip.OP_W8A16, 8192, 1024, 3072) == "dma_mfma_f16x_128x256"
