@@ -257,7 +257,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   // per-lane offset, which keeps the address state of the kLPW streams small.
   const char* wbase = reinterpret_cast<const char*>(qw);
   const char* xbase = static_cast<const char*>(xv);
-  int soff[C::kLPW];
+  uint32_t soff[C::kLPW];
   constexpr int kWCh = KS / 16, kXCh = C::kXRb / 16;   // 16-byte chunks per block row
   auto set_sources = [&](int m0, int n0, int kb) {
     wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K + (int64_t)kb * C::kKStage;
@@ -286,7 +286,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       const int b = j * C::kWaves + wave;
       const bool wblk = b < C::kWBlk;
       const int step = wblk ? KS : C::kXRow;
-      const char* p = (wblk ? wbase : xbase) + soff[j] + (int64_t)kt * step;
+      // uniform 64-bit base + unsigned 32-bit lane offset: the saddr form of
+      // the DMA, so no 64-bit address per op stays live in VGPRs
+      const char* p = (wblk ? wbase : xbase) + (uint32_t)(soff[j] + (uint32_t)(kt * step));
       __builtin_amdgcn_global_load_lds(TVQ_GPTR(p), TVQ_LPTR(stage + b * 1024), 16, 0, 0);
     }
   };
