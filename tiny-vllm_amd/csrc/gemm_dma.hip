@@ -4,7 +4,8 @@
 // Table (measured on MI355X over the BASELINE shapes; tile = BM x BN, waves,
 // ring depth S, MFMA shape):
 //   W8A8  >= 256 256x256 tiles          256x256, 8 waves (2x4), S=2, 32x32x32 i8
-//         >= 200 256x128 tiles          256x128, 8 waves (4x2), S=2, 32x32x32 i8
+//         >= 200 256x128 tiles          256x128, 8 waves (4x2), S=3, 32x32x32 i8 (one tile per CU
+//                                        at N = 1024: nothing else hides the stage latency)
 //         M > 256, or split-K M > 32,    64x64,   4 waves,       S=4, 16x16x64 i8
 //         or 64 < M with >= 256 such tiles
 //         32 < M <= 64, N >= 16384       64x128,  8 waves (2x4), S=4, 16x16x64 i8
@@ -48,7 +49,7 @@ struct CfgInfo {
 };
 constexpr CfgInfo kInfo[] = {
     {true, 256, 256, 2, 4, 2, 32, 128, "dma_mfma_i8_256x256", "dma_mfma_i8_256x256_splitk"},
-    {true, 256, 128, 4, 2, 2, 32, 128, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk"},
+    {true, 256, 128, 4, 2, 3, 32, 128, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk"},
     {true, 64, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_64x64", "dma_mfma_i8_64x64_splitk"},
     {true, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_i8_64x128", "dma_mfma_i8_64x128_splitk"},
     {true, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_32x64", "dma_mfma_i8_32x64_splitk"},
