@@ -175,7 +175,10 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
 
 }  // namespace
 
-bool dma_shape_ok(int64_t K) { return K % 128 == 0; }
+// K % 128 == 0 (whole stages), and K <= 2^22 so that every per-lane DMA
+// source offset (tile row x row bytes + stage offset, at most 256 x 2K bytes)
+// fits the unsigned 32-bit lane offset of the saddr-form loads.
+bool dma_shape_ok(int64_t K) { return K % 128 == 0 && K <= (int64_t(1) << 22); }
 
 int dma_splits(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes) {
   static char probe;  // any non-null address: only the size is consulted
