@@ -18,11 +18,14 @@
 // DMA still reads whole 128-byte lines. (With KS = 64 a block holds 16 rows
 // x 64 bytes and the same reasoning gives swz(row) = (row/4) % 4.)
 //
-// Fragment reads (one ds_read_b128 per lane, lane = 16*g + r):
+// Fragment reads (one ds_read_b128 per lane; 16x16 MFMA tiles, lane =
+// 16*g + r):
 //   weight / int8 activation, 64-k sub-step ks: row r, chunk 4*ks + g
 //     (k = 64*ks + 16g .. +16)
 //   16-bit activation (two blocks per 8 rows: k 0-63 and 64-127), sub-step
 //     ks, half b: row r, chunk 2g + b of block ks (k = 64*ks + 16g + 8b .. +8)
+// With 32x32 MFMA tiles (lane = 32*g + r) the sub-steps are 32 k wide and
+// lane group g reads chunk 2*ks + g of row r in the same way.
 // For W8A16 the 16 int8 weights of a lane (k = 16g..16g+15) are converted to
 // two 8-element bf16/fp16 halves; half b pairs with activation half b, which
 // holds the same 8 k values. Any consistent k assignment gives the same dot
@@ -32,7 +35,10 @@
 //
 // Row indices past M or N are clamped to the last row: those rows only feed
 // output rows/columns that are never stored. K must be a multiple of 128
-// (checked by the dispatcher), so no K tail is read.
+// (checked by the dispatcher), so no K tail is read. A DMA source is a
+// wave-uniform tile base in scalar registers plus an unsigned 32-bit lane
+// offset (the saddr form, no 64-bit address per op in VGPRs); the
+// dispatcher's K <= 2^22 keeps those offsets within 32 bits.
 //
 // Waits are explicit: the compiler does not track LDS-DMA completion, so each
 // step waits on vmcnt for its own stage and then crosses an s_barrier (a bare
