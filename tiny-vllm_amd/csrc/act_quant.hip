@@ -71,12 +71,12 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
   for (int it = 0; it < kCacheIters; ++it) {
     const int64_t v = (int64_t)it * kWave + lane;
     if (v < nvec) {
-      cache[it] = ldg128(xr + v * 8);
+      cache[it] = ldg128_stream(xr + v * 8);
       amax = fmaxf(amax, absmax8<T>(cache[it]));
     }
   }
   for (int64_t v = (int64_t)kCacheIters * kWave + lane; v < nvec; v += kWave) {
-    amax = fmaxf(amax, absmax8<T>(ldg128(xr + v * 8)));
+    amax = fmaxf(amax, absmax8<T>(ldg128_stream(xr + v * 8)));
   }
   amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);

@@ -104,9 +104,9 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __rest
   for (int it = 0; it < kIters; ++it) {
     const int v = it * kWave + lane;
     if (v < nvec) {
-      const u32x4 xv = ldg128(xr + (int64_t)v * 8);
+      const u32x4 xv = ldg128_stream(xr + (int64_t)v * 8);
       u32x4 rv = {0, 0, 0, 0};
-      if constexpr (kRes) rv = ldg128(res + row * K + (int64_t)v * 8);
+      if constexpr (kRes) rv = ldg128_stream(res + row * K + (int64_t)v * 8);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float t = elt<T>(xv, i);
@@ -157,8 +157,8 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __res
   for (int it = 0; it < kIters; ++it) {
     const int v = it * kWave + lane;
     if (v < nvec) {
-      const u32x4 gv = ldg128(g + (int64_t)v * 8);
-      const u32x4 uv = ldg128(u + (int64_t)v * 8);
+      const u32x4 gv = ldg128_stream(g + (int64_t)v * 8);
+      const u32x4 uv = ldg128_stream(u + (int64_t)v * 8);
       float o[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {

@@ -87,8 +87,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
     if (slot >= 0 && slot < num_slots && pos >= 0 && pos < max_len)
       cache_row = (h < Hq + Hkv ? k_cache : v_cache) + ((slot * Hkv + kvh) * (int64_t)max_len + pos) * kD;
   }
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(src + 4 * j);
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 64 + 4 * j);
+  // read once: non-temporal
+  const u32x2 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + 4 * j));
+  const u32x2 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + 64 + 4 * j));
   if (h >= Hq + Hkv) {  // value head: copy to the cache only
     if (cache_row) {
       *reinterpret_cast<u32x2*>(cache_row + 4 * j) = lo;

@@ -123,8 +123,9 @@ __device__ __forceinline__ u32x4 ldg128(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
-// Streaming (read-once) 128-bit load: non-temporal so weights that are read
-// exactly once do not evict the activations other workgroups re-read.
+// Streaming (read-once) 128-bit load: non-temporal, for data each kernel
+// reads exactly once (GEMV weights, producer and act-quant inputs), so it
+// does not evict what other workgroups re-read.
 __device__ __forceinline__ u32x4 ldg128_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
