@@ -142,10 +142,19 @@ hipError_t go(const GemmArgs& a, hipStream_t s) {
   // Unsplit launches use the instantiation without the split-K fixup (fewer
   // registers; measured ~4 % faster on the M=256 headline shape).
   if constexpr (splittable<c>()) {
+    // W8A8 at decode-size M (<= 64, one or two m-tiles): each weight byte is
+    // read by at most two workgroups, so the weight stream takes the
+    // non-temporal hint
+    // (measured 2-5 % on the decode shapes; W8A16 gained nothing).
+    constexpr bool kNt = i.w8a8;
     if (splits > 1)
-      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, true>(
+      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, true, kNt>(
           a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), splits,
           a.workspace, a.workspace_bytes, s);
+    if (kNt && a.M <= 64)
+      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false, kNt>(
+          a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr,
+          0, s);
   }
   return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false>(
       a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0,

@@ -222,7 +222,8 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
   }
 }
 
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit>
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
+          bool kNtW = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
@@ -295,7 +296,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       // uniform 64-bit base + unsigned 32-bit lane offset: the saddr form of
       // the DMA, so no 64-bit address per op stays live in VGPRs
       const char* p = (wblk ? wbase : xbase) + (uint32_t)(soff[j] + (uint32_t)(kt * step));
-      __builtin_amdgcn_global_load_lds(TVQ_GPTR(p), TVQ_LPTR(stage + b * 1024), 16, 0, 0);
+      // kNtW: weight blocks that no other tile reads again (one m-tile)
+      // stream with the non-temporal hint, so they do not evict the
+      // activation panel every tile shares from L2
+      if (kNtW && wblk)
+        __builtin_amdgcn_global_load_lds(TVQ_GPTR(p), TVQ_LPTR(stage + b * 1024), 16, 0, 2);
+      else
+        __builtin_amdgcn_global_load_lds(TVQ_GPTR(p), TVQ_LPTR(stage + b * 1024), 16, 0, 0);
     }
   };
 
@@ -694,12 +701,13 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
   return (nk + per - 1) / per;
 }
 
-template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit>
+template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
+          bool kNtW = false>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
                       int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
                       hipStream_t stream) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
-  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
