@@ -20,9 +20,11 @@ Owns the model, the KV cache and the sampler:
 """
 from __future__ import annotations
 
+import itertools
 import os
 from glob import glob
 
+import numpy as np
 import torch
 from torch import nn
 
@@ -175,22 +177,31 @@ class ModelRunner:
     @torch.no_grad()
     def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
         if is_prefill:
-            ids, pos, cu = [], [], [0]
-            for s in seqs:
-                ids.extend(s.token_ids)
-                pos.extend(range(len(s)))
-                cu.append(cu[-1] + len(s))
-            lmax = max(len(s) for s in seqs)
+            # Per-token inputs are built with array ops: only the token ids
+            # cross from Python (one fromiter); positions and per-token slots
+            # expand from the per-sequence lengths on the device. The list
+            # loops they replace cost ~5 ms of host time per 16k tokens,
+            # during which the GPU had nothing queued.
+            lens = [len(s) for s in seqs]
+            cu = [0, *itertools.accumulate(lens)]
+            total = cu[-1]
+            ids = torch.from_numpy(np.fromiter(itertools.chain.from_iterable(s.token_ids for s in seqs),
+                                               dtype=np.int64, count=total))
+            lmax = max(lens)
+            lens_t = self._to_gpu(lens, torch.int64)
+            starts = self._to_gpu(cu[:-1], torch.int64)
+            pos = torch.arange(total, device=lens_t.device) - torch.repeat_interleave(starts, lens_t, output_size=total)
             if self.device == "cuda":
-                blocks = _hip.prefill_blocks([(cu[i], len(s)) for i, s in enumerate(seqs)])
-                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
-                            slot_mapping=self._to_gpu([s.slot for s in seqs], torch.int64),
+                blocks = _hip.prefill_blocks([(cu[i], n) for i, n in enumerate(lens)])
+                slots = self._to_gpu([s.slot for s in seqs], torch.int64)
+                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax, slot_mapping=slots,
                             attn_blocks=blocks.pin_memory().cuda(non_blocking=True),
-                            token_slots=self._to_gpu([s.slot for s in seqs for _ in range(len(s))], torch.int64))
+                            token_slots=torch.repeat_interleave(slots, lens_t, output_size=total))
+                ids = ids.pin_memory().cuda(non_blocking=True)
             else:
                 set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
                             slot_mapping=torch.tensor([s.slot for s in seqs]))
-            hidden = self.model(self._to_gpu(ids, torch.int64), self._to_gpu(pos, torch.int64))
+            hidden = self.model(ids, pos)
             hidden = hidden[self._to_gpu(cu[1:], torch.int64) - 1]
         elif self.graphs and len(seqs) <= self.graph_bs[-1]:
             hidden = self._replay_decode(seqs)
