@@ -11,9 +11,12 @@
 //
 // One wave (64 lanes) owns one row; a 256-thread workgroup handles 4 rows.
 // HBM traffic is the algorithmic minimum for rows that fit the register
-// cache (K <= 64 * 8 * kCacheIters): 2 B read + 1 B written per element and
+// cache (K <= 64 * 8 * NI, NI = 1, 2, 4 or 8 by K, so short rows keep few
+// VGPRs and many waves in flight): 2 B read + 1 B written per element and
 // 4 B per row. Longer rows are read a second time for the quantize pass
-// (that second read is served by L2).
+// (that second read is served by L2). Codes take quant_code_fast; a vector
+// step in which any lane met a near-tie is redone with the exact quant_code
+// (a few percent of steps), which keeps the common path branch-free.
 #include "tvq_common.h"
 #include "tvq_internal.h"
 
@@ -21,7 +24,7 @@ namespace tvq {
 namespace {
 
 constexpr int kRowsPerBlock = 4;
-constexpr int kCacheIters = 8;  // 8 x 512 elements -> K <= 4096 stays in VGPRs
+constexpr int kMaxIters = 8;  // 8 x 512 elements -> K <= 4096 stays in VGPRs
 
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
@@ -44,6 +47,28 @@ __device__ __forceinline__ uint32_t q1(float x, float s, float rs) {
 }
 
 template <typename T>
+__device__ __forceinline__ uint32_t q1f(const u32x4& v, int i, float rs, bool& near) {
+  const uint32_t w = v[i >> 1];
+  const float x = to_float<T>((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+  return (uint32_t)((int32_t)quant_code_fast(x, rs, near) & 0xff);
+}
+
+// 8 codes, exact: fast codes unless some lane of the wave met a near-tie.
+template <typename T>
+__device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs);
+template <typename T>
+__device__ __forceinline__ u32x2 quant8_wave(u32x4 v, float s, float rs) {
+  bool near = false;
+  u32x2 r;
+  r.x = q1f<T>(v, 0, rs, near) | (q1f<T>(v, 1, rs, near) << 8) | (q1f<T>(v, 2, rs, near) << 16) |
+        (q1f<T>(v, 3, rs, near) << 24);
+  r.y = q1f<T>(v, 4, rs, near) | (q1f<T>(v, 5, rs, near) << 8) | (q1f<T>(v, 6, rs, near) << 16) |
+        (q1f<T>(v, 7, rs, near) << 24);
+  if (__builtin_amdgcn_ballot_w64(near) != 0) r = quant8<T>(v, s, rs);  // wave-uniform
+  return r;
+}
+
+template <typename T>
 __device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs) {
   u32x2 r;
   r.x = q1(to_float<T>((uint16_t)(v[0] & 0xffffu)), s, rs) | (q1(to_float<T>((uint16_t)(v[0] >> 16)), s, rs) << 8) |
@@ -54,7 +79,7 @@ __device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs) {
 }
 
 // Vector path: K % 8 == 0 and 16-byte aligned x, 8-byte aligned xq.
-template <typename T>
+template <typename T, int NI>
 __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                             float eps, int8_t* __restrict__ xq,
                                                             float* __restrict__ a_scales) {
@@ -65,17 +90,18 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
   int8_t* qr = xq + row * K;
   const int64_t nvec = K >> 3;  // 8 elements per 16-byte vector
 
-  u32x4 cache[kCacheIters];
+  u32x4 cache[NI];
   float amax = 0.0f;
 #pragma unroll
-  for (int it = 0; it < kCacheIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     const int64_t v = (int64_t)it * kWave + lane;
+    cache[it] = u32x4{0, 0, 0, 0};  // lanes past the row quantize zeros (no near-tie)
     if (v < nvec) {
       cache[it] = ldg128_stream(xr + v * 8);
       amax = fmaxf(amax, absmax8<T>(cache[it]));
     }
   }
-  for (int64_t v = (int64_t)kCacheIters * kWave + lane; v < nvec; v += kWave) {
+  for (int64_t v = (int64_t)NI * kWave + lane; v < nvec; v += kWave) {
     amax = fmaxf(amax, absmax8<T>(ldg128_stream(xr + v * 8)));
   }
   amax = wave_max(amax);
@@ -84,12 +110,17 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
   const float rs = __fdiv_rn(1.0f, s);
 
 #pragma unroll
-  for (int it = 0; it < kCacheIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     const int64_t v = (int64_t)it * kWave + lane;
-    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = quant8<T>(cache[it], s, rs);
+    if (it * kWave < nvec) {  // wave-uniform: the ballot needs every active lane
+      const u32x2 c = quant8_wave<T>(cache[it], s, rs);
+      if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = c;
+    }
   }
-  for (int64_t v = (int64_t)kCacheIters * kWave + lane; v < nvec; v += kWave) {
-    *reinterpret_cast<u32x2*>(qr + v * 8) = quant8<T>(ldg128(xr + v * 8), s, rs);
+  for (int64_t v0 = (int64_t)NI * kWave; v0 < nvec; v0 += kWave) {
+    const int64_t v = v0 + lane;
+    const u32x2 c = quant8_wave<T>(v < nvec ? ldg128(xr + v * 8) : u32x4{0, 0, 0, 0}, s, rs);
+    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = c;
   }
 }
 
@@ -123,10 +154,15 @@ hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, floa
   const dim3 block(256);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   if (act_quant_vec_ok(x, xq, K)) {
-    if (bf16)
-      act_quant_vec_kernel<BF16><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales);
-    else
-      act_quant_vec_kernel<F16><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+    // register cache sized to the row: 512 elements per iteration
+#define TVQ_AQ(NI)                                                                    \
+  (bf16 ? act_quant_vec_kernel<BF16, NI><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales) \
+        : act_quant_vec_kernel<F16, NI><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales))
+    if (K <= 512) TVQ_AQ(1);
+    else if (K <= 1024) TVQ_AQ(2);
+    else if (K <= 2048) TVQ_AQ(4);
+    else TVQ_AQ(kMaxIters);
+#undef TVQ_AQ
   } else {
     if (bf16)
       act_quant_scalar_kernel<BF16><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales);

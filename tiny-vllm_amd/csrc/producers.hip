@@ -25,6 +25,8 @@
 // and y (2 B/elem) and/or the codes (1 B/elem) + 4 B per row. Longer rows or
 // K % 8 != 0 or unaligned pointers take a scalar path that re-reads the row
 // (from L2).
+#include <type_traits>
+
 #include "tvq_common.h"
 #include "tvq_internal.h"
 
@@ -32,7 +34,7 @@ namespace tvq {
 namespace {
 
 constexpr int kRows = 4;
-constexpr int kIters = 8;  // 8 x 64 lanes x 8 elements = 4096
+constexpr int kIters = 8;  // at most 8 x 64 lanes x 8 elements = 4096 per row in registers
 
 __device__ __forceinline__ float wsum(float v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -57,13 +59,14 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 // Quantize the 8-element bf16/fp16 vectors cached in y[] (already rounded)
-// and store codes + scale.
-template <typename T>
-__device__ __forceinline__ void quant_store(const u32x4 (&y)[kIters], int nvec, int lane, float eps, int8_t* qr,
+// and store codes + scale. Codes take quant_code_fast; a vector step where
+// any lane met a near-tie is redone with the exact quant_code.
+template <typename T, int NI>
+__device__ __forceinline__ void quant_store(const u32x4 (&y)[NI], int nvec, int lane, float eps, int8_t* qr,
                                             float* srow) {
   float amax = 0.0f;
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     if (it * kWave + lane < nvec) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(elt<T>(y[it], i)));
@@ -74,21 +77,38 @@ __device__ __forceinline__ void quant_store(const u32x4 (&y)[kIters], int nvec, 
   if (lane == 0) *srow = s;
   const float rs = __fdiv_rn(1.0f, s);
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     const int v = it * kWave + lane;
-    if (v < nvec) {
+    if (it * kWave < nvec) {  // wave-uniform: the ballot needs every active lane
+      const u32x4 yv = v < nvec ? y[it] : u32x4{0, 0, 0, 0};
+      bool near = false;
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        lo |= (uint32_t)(uint8_t)qcode(elt<T>(y[it], i), s, rs) << (8 * i);
-        hi |= (uint32_t)(uint8_t)qcode(elt<T>(y[it], i + 4), s, rs) << (8 * i);
+        lo |= ((uint32_t)(int32_t)quant_code_fast(elt<T>(yv, i), rs, near) & 0xffu) << (8 * i);
+        hi |= ((uint32_t)(int32_t)quant_code_fast(elt<T>(yv, i + 4), rs, near) & 0xffu) << (8 * i);
       }
-      *reinterpret_cast<u32x2*>(qr + (int64_t)v * 8) = u32x2{lo, hi};
+      if (__builtin_amdgcn_ballot_w64(near) != 0) {
+        lo = hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo |= (uint32_t)(uint8_t)qcode(elt<T>(yv, i), s, rs) << (8 * i);
+          hi |= (uint32_t)(uint8_t)qcode(elt<T>(yv, i + 4), s, rs) << (8 * i);
+        }
+      }
+      if (v < nvec) *reinterpret_cast<u32x2*>(qr + (int64_t)v * 8) = u32x2{lo, hi};
     }
   }
 }
 
-template <typename T, bool kRes, bool kY, bool kQ>
+// SiLU(a) = a / (1 + exp(-a)) = a * rcp(1 + 2^(-a log2 e)), on the hardware
+// exp2 and reciprocal (about 1 ulp each in fp32; the bf16/fp16 result is
+// then rounded once, as the reference's fused elementwise kernel rounds).
+__device__ __forceinline__ float silu_f(float a) {
+  return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
+}
+
+template <typename T, bool kRes, bool kY, bool kQ, int NI>
 __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
                                                           const uint16_t* __restrict__ w, float eps,
                                                           uint16_t* __restrict__ y, int8_t* __restrict__ xq,
@@ -98,10 +118,10 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __rest
   if (row >= M) return;
   const int nvec = K >> 3;
   const uint16_t* xr = x + row * K;
-  float h[kIters][8];
+  float h[NI][8];
   float ss = 0.0f;
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     const int v = it * kWave + lane;
     if (v < nvec) {
       const u32x4 xv = ldg128_stream(xr + (int64_t)v * 8);
@@ -124,9 +144,9 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __rest
   }
   ss = wsum(ss);
   const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)K) + eps));
-  u32x4 yv[kIters];
+  u32x4 yv[NI];
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     const int v = it * kWave + lane;
     if (v < nvec) {
       const u32x4 wv = ldg128(w + (int64_t)v * 8);
@@ -139,10 +159,10 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __rest
       if constexpr (kY) *reinterpret_cast<u32x4*>(y + row * K + (int64_t)v * 8) = yv[it];
     }
   }
-  if constexpr (kQ) quant_store<T>(yv, nvec, lane, 1e-8f, xq + row * K, a_scales + row);
+  if constexpr (kQ) quant_store<T, NI>(yv, nvec, lane, 1e-8f, xq + row * K, a_scales + row);
 }
 
-template <typename T, bool kY, bool kQ>
+template <typename T, bool kY, bool kQ, int NI>
 __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ y,
                                                            int8_t* __restrict__ xq, float* __restrict__ a_scales,
                                                            int64_t M, int I) {
@@ -152,9 +172,9 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __res
   const int nvec = I >> 3;
   const uint16_t* g = gu + row * 2 * I;
   const uint16_t* u = g + I;
-  u32x4 yv[kIters];
+  u32x4 yv[NI];
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
+  for (int it = 0; it < NI; ++it) {
     const int v = it * kWave + lane;
     if (v < nvec) {
       const u32x4 gv = ldg128_stream(g + (int64_t)v * 8);
@@ -163,14 +183,14 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __res
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float a = elt<T>(gv, i);
-        o[i] = __fdiv_rn(a, 1.0f + expf(-a)) * elt<T>(uv, i);
+        o[i] = silu_f(a) * elt<T>(uv, i);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) yv[it][i] = pack2<T>(o[2 * i], o[2 * i + 1]);
       if constexpr (kY) *reinterpret_cast<u32x4*>(y + row * I + (int64_t)v * 8) = yv[it];
     }
   }
-  if constexpr (kQ) quant_store<T>(yv, nvec, lane, 1e-8f, xq + row * I, a_scales + row);
+  if constexpr (kQ) quant_store<T, NI>(yv, nvec, lane, 1e-8f, xq + row * I, a_scales + row);
 }
 
 // ---------------------------------------------------------------- scalar paths
@@ -234,7 +254,7 @@ __global__ __launch_bounds__(256) void silu_mul_scalar_kernel(const uint16_t* __
   const uint16_t* g = gu + row * 2 * I;
   auto val = [&](int k) {
     const float a = to_float<T>(g[k]);
-    return to_float<T>(from_float<T>(__fdiv_rn(a, 1.0f + expf(-a)) * to_float<T>(g[I + k])));
+    return to_float<T>(from_float<T>(silu_f(a) * to_float<T>(g[I + k])));
   };
   float amax = 0.0f;
   for (int k = lane; k < I; k += kWave) {
@@ -270,18 +290,26 @@ static hipError_t rms_t(const void* x, void* res, const void* w, float eps, void
     rmsnorm_scalar_kernel<T><<<grid, block, 0, st>>>(X, R, W, eps, Y, xq, as, M, k);
     return hipGetLastError();
   }
-#define TVQ_RMS(RES, YY, QQ) rmsnorm_vec_kernel<T, RES, YY, QQ><<<grid, block, 0, st>>>(X, R, W, eps, Y, xq, as, M, k)
   const bool hy = y != nullptr, hq = xq != nullptr;
-  if (res) {
-    if (hy && hq) TVQ_RMS(true, true, true);
-    else if (hy) TVQ_RMS(true, true, false);
-    else TVQ_RMS(true, false, true);
-  } else {
-    if (hy && hq) TVQ_RMS(false, true, true);
-    else if (hy) TVQ_RMS(false, true, false);
-    else TVQ_RMS(false, false, true);
-  }
+  // row held in registers: NI iterations of 512 elements, sized to K
+  auto go = [&](auto ni) {
+    constexpr int NI = decltype(ni)::value;
+#define TVQ_RMS(RES, YY, QQ) \
+  rmsnorm_vec_kernel<T, RES, YY, QQ, NI><<<grid, block, 0, st>>>(X, R, W, eps, Y, xq, as, M, k)
+    if (res) {
+      if (hy && hq) TVQ_RMS(true, true, true);
+      else if (hy) TVQ_RMS(true, true, false);
+      else TVQ_RMS(true, false, true);
+    } else {
+      if (hy && hq) TVQ_RMS(false, true, true);
+      else if (hy) TVQ_RMS(false, true, false);
+      else TVQ_RMS(false, false, true);
+    }
 #undef TVQ_RMS
+  };
+  if (K <= 1024) go(std::integral_constant<int, 2>{});
+  else if (K <= 2048) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, kIters>{});
   return hipGetLastError();
 }
 
@@ -301,9 +329,16 @@ static hipError_t silu_t(const void* gu, void* y, int8_t* xq, float* as, int64_t
     silu_mul_scalar_kernel<T><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
     return hipGetLastError();
   }
-  if (y && xq) silu_mul_vec_kernel<T, true, true><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
-  else if (y) silu_mul_vec_kernel<T, true, false><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
-  else silu_mul_vec_kernel<T, false, true><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
+  auto go = [&](auto ni) {
+    constexpr int NI = decltype(ni)::value;
+    if (y && xq) silu_mul_vec_kernel<T, true, true, NI><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
+    else if (y) silu_mul_vec_kernel<T, true, false, NI><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
+    else silu_mul_vec_kernel<T, false, true, NI><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
+  };
+  if (I <= 1024) go(std::integral_constant<int, 2>{});
+  else if (I <= 2048) go(std::integral_constant<int, 4>{});
+  else if (I <= 3072) go(std::integral_constant<int, 6>{});
+  else go(std::integral_constant<int, kIters>{});
   return hipGetLastError();
 }
 

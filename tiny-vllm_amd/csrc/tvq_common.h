@@ -160,4 +160,14 @@ __device__ __forceinline__ float quant_code(float x, float s, float rs) {
   return fminf(fmaxf(t, -127.0f), 127.0f);
 }
 
+// quant_code without its rare branch: rint(x * rs) clamped, and `near` set
+// when x * rs lies within 2^-14 of a half-integer. Callers OR `near` over a
+// wave (ballot) and redo those vectors with quant_code, so the common path
+// stays branch-free and bit-identical to quant_code.
+__device__ __forceinline__ float quant_code_fast(float x, float rs, bool& near) {
+  const float d = x * rs;
+  near |= fabsf(fabsf(d - truncf(d)) - 0.5f) < 0x1p-14f;
+  return fminf(fmaxf(rintf(d), -127.0f), 127.0f);
+}
+
 }  // namespace tvq
