@@ -200,7 +200,8 @@ int tvq_decode_attention(const void* q, int64_t q_stride, const void* k_new,
  *          (slots[t], positions[t]) of the caches, replacing store_kvcache
  *          (attention.py:10-40) for prompt tokens; tokens whose slot or
  *          position is out of range are not stored.
- * head_dim must be 128. */
+ * head_dim must be 128; every pointer 16-byte aligned and row_stride a
+ * multiple of 8 elements (TVQ_E_UNSUPPORTED otherwise). */
 int tvq_qk_norm_rope(const void* qkv, int64_t row_stride,
                      const int64_t* positions, const float* cos_t,
                      const float* sin_t, const void* q_weight,

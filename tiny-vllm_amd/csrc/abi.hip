@@ -266,13 +266,12 @@ int tvq_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positio
     return fail(TVQ_E_INVALID, "invalid num_slots / max_len");
   if (row_stride < (int64_t)(Hq + (store ? 2 : 1) * Hkv) * head_dim)
     return fail(TVQ_E_INVALID, "row_stride shorter than the heads read");
-  if (T * (Hq + 2 * Hkv) / 16 + 1 > kMaxDim) return fail(TVQ_E_UNSUPPORTED, "too many (token, head) pairs");
-  // 8-byte accesses (16 for the fp32 cos/sin rows)
-  auto a8 = [](const void* p) { return ((uintptr_t)p & 7u) == 0; };
-  if (!a8(qkv) || row_stride % 4 || !a8(q_out) || !a8(k_out) || !a8(q_weight) || !a8(k_weight) || !a8(k_cache) ||
-      !a8(v_cache) || !aligned16(cos_t) || !aligned16(sin_t))
-    return fail(TVQ_E_UNSUPPORTED, "qk_norm_rope needs 8-byte aligned rows (row_stride %% 4 == 0) and 16-byte "
-                                   "aligned cos/sin tables");
+  if (T * (Hq + 2 * Hkv) / 32 + 1 > kMaxDim) return fail(TVQ_E_UNSUPPORTED, "too many (token, head) pairs");
+  // 16-byte accesses throughout
+  if (!aligned16(qkv) || row_stride % 8 || !aligned16(q_out) || !aligned16(k_out) || !aligned16(q_weight) ||
+      !aligned16(k_weight) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(cos_t) || !aligned16(sin_t))
+    return fail(TVQ_E_UNSUPPORTED, "qk_norm_rope needs 16-byte aligned rows (row_stride %% 8 == 0), outputs, "
+                                   "weights, caches and cos/sin tables");
   hipError_t e = launch_qk_norm_rope(qkv, row_stride, positions, cos_t, sin_t, q_weight, k_weight, eps, T, Hq, Hkv,
                                      (int)max_pos, q_out, k_out, k_cache, v_cache, slots, (int)num_slots,
                                      (int)max_len, dtype == TVQ_DTYPE_BF16, (hipStream_t)stream);

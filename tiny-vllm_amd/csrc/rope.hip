@@ -9,11 +9,11 @@
 // with fp32 temporaries, by one launch that reads q and k once from the packed
 // qkv projection output and writes them once.
 //
-// Sixteen lanes per (token, head), head_dim D = 128: lane j of the group
-// holds x[4j..4j+3] and x[64+4j..64+4j+3], exactly the pairs the rotate-half
-// rotation mixes, so the rotation is lane-local, every access is 8 bytes per
-// lane (16 for the fp32 cos/sin rows) and the RMS statistic is a 16-lane
-// reduction. Four heads per wave.
+// Eight lanes per (token, head), head_dim D = 128: lane j of the group
+// holds x[8j..8j+7] and x[64+8j..64+8j+7], exactly the pairs the rotate-half
+// rotation mixes, so the rotation is lane-local, every access is 16 bytes
+// per lane (32 for the fp32 cos/sin rows) and the RMS statistic is an
+// 8-lane reduction. Eight heads per wave.
 // Rounding follows the reference step by step:
 //   n  = round(x * rsqrt(mean(x^2) + eps))     (fp32, IEEE sqrt and divide)
 //   n  = round(n * w)                           (bf16 x bf16 -> one rounding)
@@ -33,7 +33,7 @@ namespace tvq {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kGroup = 16;                  // lanes per head
+constexpr int kGroup = 8;                   // lanes per head
 constexpr int kItemsPerBlock = 256 / kGroup;
 
 __device__ __forceinline__ float group_sum(float v) {
@@ -41,19 +41,20 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Four 16-bit values <-> floats.
+// Eight 16-bit values <-> floats.
 template <typename T>
-__device__ __forceinline__ void unpack4(u32x2 w, float (&f)[4]) {
-  f[0] = to_float<T>((uint16_t)w.x);
-  f[1] = to_float<T>((uint16_t)(w.x >> 16));
-  f[2] = to_float<T>((uint16_t)w.y);
-  f[3] = to_float<T>((uint16_t)(w.y >> 16));
+__device__ __forceinline__ void unpack8(u32x4 w, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = to_float<T>((uint16_t)w[i]);
+    f[2 * i + 1] = to_float<T>((uint16_t)(w[i] >> 16));
+  }
 }
 template <typename T>
-__device__ __forceinline__ u32x2 pack4(const float (&f)[4]) {
-  u32x2 w;
-  w.x = (uint32_t)from_float<T>(f[0]) | ((uint32_t)from_float<T>(f[1]) << 16);
-  w.y = (uint32_t)from_float<T>(f[2]) | ((uint32_t)from_float<T>(f[3]) << 16);
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)from_float<T>(f[2 * i]) | ((uint32_t)from_float<T>(f[2 * i + 1]) << 16);
   return w;
 }
 
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
   const int64_t item = (int64_t)blockIdx.x * kItemsPerBlock + (threadIdx.x / kGroup);
   const bool store = k_cache != nullptr;
   const int heads = Hq + Hkv + (store ? Hkv : 0);
-  if (item >= (int64_t)T_ * heads) return;  // whole 16-lane groups leave together
+  if (item >= (int64_t)T_ * heads) return;  // whole 8-lane groups leave together
   const int64_t t = item / heads;
   const int h = (int)(item % heads);
   const bool is_q = h < Hq;
@@ -88,51 +89,55 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
       cache_row = (h < Hq + Hkv ? k_cache : v_cache) + ((slot * Hkv + kvh) * (int64_t)max_len + pos) * kD;
   }
   // read once: non-temporal
-  const u32x2 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + 4 * j));
-  const u32x2 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + 64 + 4 * j));
+  const u32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 8 * j));
+  const u32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 64 + 8 * j));
   if (h >= Hq + Hkv) {  // value head: copy to the cache only
     if (cache_row) {
-      *reinterpret_cast<u32x2*>(cache_row + 4 * j) = lo;
-      *reinterpret_cast<u32x2*>(cache_row + 64 + 4 * j) = hi;
+      *reinterpret_cast<u32x4*>(cache_row + 8 * j) = lo;
+      *reinterpret_cast<u32x4*>(cache_row + 64 + 8 * j) = hi;
     }
     return;
   }
-  float x1[4], x2[4];
-  unpack4<T>(lo, x1);
-  unpack4<T>(hi, x2);
+  float x1[8], x2[8];
+  unpack8<T>(lo, x1);
+  unpack8<T>(hi, x2);
   if constexpr (kNorm) {
     float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+    for (int e = 0; e < 8; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
     ss = group_sum(ss);
     const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)kD) + eps));
     const uint16_t* w = is_q ? qw : kw;
-    float w1[4], w2[4];
-    unpack4<T>(*reinterpret_cast<const u32x2*>(w + 4 * j), w1);
-    unpack4<T>(*reinterpret_cast<const u32x2*>(w + 64 + 4 * j), w2);
+    float w1[8], w2[8];
+    unpack8<T>(*reinterpret_cast<const u32x4*>(w + 8 * j), w1);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(w + 64 + 8 * j), w2);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 8; ++e) {
       x1[e] = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x1[e] * r)) * w1[e]));
       x2[e] = to_float<T>(from_float<T>(to_float<T>(from_float<T>(x2[e] * r)) * w2[e]));
     }
   }
   int64_t p = positions[t];
   p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
-  const f32x4 c = *reinterpret_cast<const f32x4*>(cos_t + p * (kD / 2) + 4 * j);
-  const f32x4 sn = *reinterpret_cast<const f32x4*>(sin_t + p * (kD / 2) + 4 * j);
-  float y1[4], y2[4];
+  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cos_t + p * (kD / 2) + 8 * j);
+  const f32x4 c1 = *reinterpret_cast<const f32x4*>(cos_t + p * (kD / 2) + 8 * j + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(sin_t + p * (kD / 2) + 8 * j);
+  const f32x4 s1 = *reinterpret_cast<const f32x4*>(sin_t + p * (kD / 2) + 8 * j + 4);
+  float y1[8], y2[8];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    y1[e] = x1[e] * c[e] - x2[e] * sn[e];
-    y2[e] = x2[e] * c[e] + x1[e] * sn[e];
+  for (int e = 0; e < 8; ++e) {
+    const float c = e < 4 ? c0[e] : c1[e - 4];
+    const float sn = e < 4 ? s0[e] : s1[e - 4];
+    y1[e] = x1[e] * c - x2[e] * sn;
+    y2[e] = x2[e] * c + x1[e] * sn;
   }
   uint16_t* dst = is_q ? q_out + (t * Hq + h) * kD : k_out + (t * Hkv + (h - Hq)) * kD;
-  const u32x2 o1 = pack4<T>(y1), o2 = pack4<T>(y2);
-  *reinterpret_cast<u32x2*>(dst + 4 * j) = o1;
-  *reinterpret_cast<u32x2*>(dst + 64 + 4 * j) = o2;
+  const u32x4 o1 = pack8<T>(y1), o2 = pack8<T>(y2);
+  *reinterpret_cast<u32x4*>(dst + 8 * j) = o1;
+  *reinterpret_cast<u32x4*>(dst + 64 + 8 * j) = o2;
   if (cache_row) {
-    *reinterpret_cast<u32x2*>(cache_row + 4 * j) = o1;
-    *reinterpret_cast<u32x2*>(cache_row + 64 + 4 * j) = o2;
+    *reinterpret_cast<u32x4*>(cache_row + 8 * j) = o1;
+    *reinterpret_cast<u32x4*>(cache_row + 64 + 8 * j) = o2;
   }
 }
 
