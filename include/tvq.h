@@ -151,6 +151,24 @@ int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps,
                 void* y, int8_t* xq, float* a_scales, int dtype, int64_t M,
                 int64_t K, void* stream);
 
+/* W8A8 gate_up projection with the SiLU-and-multiply in its epilogue:
+ * y[m, c] = out(silu(g) * u) with g = out(W8A8 result of gate channel c),
+ * u = the same for up channel c, each rounded to the output type first, so
+ * y is bit-identical to tvq_w8a8_gemm of gate_up followed by tvq_silu_mul.
+ * Fuses MergedColumnParallelLinear(gate_up_proj) with SiluAndMul
+ * (nanovllm/layers/activation.py:11-14); the gate_up output [M, 2I] never
+ * reaches HBM. qweight_glu / w_scales_glu are gate_up's [2I, K] weights and
+ * scales with their rows regrouped in 32-row blocks: block 2b holds gate
+ * channels 32b .. 32b+31, block 2b+1 the up channels 32b .. 32b+31
+ * (rows 64b + 32h + k <- gate_up row h*I + 32b + k). N2 = 2I must be a
+ * multiple of 64, K a multiple
+ * of 128 (at most 2^22); all pointers 16-byte aligned; y is [M, I] of
+ * out_dtype. No workspace. */
+int tvq_w8a8_gemm_glu(const int8_t* xq, const float* a_scales,
+                      const int8_t* qweight_glu, const float* w_scales_glu,
+                      void* y, int out_dtype, int64_t M, int64_t N2, int64_t K,
+                      void* stream);
+
 /* Fused SiLU-and-multiply producer of the down_proj input. Replaces
  * SiluAndMul.forward (nanovllm/layers/activation.py:11-14) on gate_up
  * [M, 2*I] (gate = columns [0, I), up = [I, 2I)): y = silu(gate) * up,

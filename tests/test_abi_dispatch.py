@@ -65,6 +65,14 @@ def test_abi_version_and_errors_without_gpu(hiplib):
     assert hiplib.tvq_silu_mul(1, None, 1, None, 1, 4, 16, None) == -1
     assert b"without a_scales" in hiplib.tvq_last_error()
     assert hiplib.tvq_silu_mul(1, 1, None, None, 1, 0, 16, None) == 0
+    assert hiplib.tvq_w8a8_gemm_glu(None, None, None, None, None, 1, 4, 128, 128, None) == -1
+    assert b"null pointer" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a8_gemm_glu(16, 16, 16, 16, 16, 1, 4, 96, 128, None) == -2
+    assert b"N2 % 64" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a8_gemm_glu(16, 16, 16, 16, 16, 1, 4, 128, 100, None) == -2
+    assert hiplib.tvq_w8a8_gemm_glu(16, 16, 16, 16, 8, 1, 4, 128, 128, None) == -2
+    assert b"16-byte aligned" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a8_gemm_glu(None, None, None, None, None, 1, 0, 128, 128, None) == 0
     # M == 0 is a valid no-op that launches nothing
     assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 0, 8, 16, None, 0, None) == 0
     assert hiplib.tvq_last_error() == b""
@@ -249,3 +257,19 @@ def test_prefill_block_size_matches_header():
     assert int(re.search(r"#define TVQ_PREFILL_BLOCK_Q (\d+)", hdr).group(1)) == _hip.PREFILL_BLOCK_Q
     rows = _hip.prefill_blocks([(0, 130), (130, 64)]).tolist()
     assert sorted(r[2] for r in rows if r[0] == 0) == list(range(0, 130, _hip.PREFILL_BLOCK_Q))
+
+
+def test_glu_interleave_layout():
+    """Row 64b + 32h + k of the regrouped gate_up weights is old row h*I + 32b + k."""
+    from nanovllm.quantization import _hip
+    i, k = 96, 8
+    qw = torch.arange(2 * i * k, dtype=torch.int32).view(2 * i, k).to(torch.int8)
+    rows = torch.arange(2 * i, dtype=torch.float32)
+    q2, s2 = _hip.glu_interleave(qw, rows)
+    for b in range(i // 32):
+        for h in range(2):
+            for kk in range(32):
+                assert s2[64 * b + 32 * h + kk].item() == h * i + 32 * b + kk
+    assert torch.equal(q2, qw[s2.long()])
+    with pytest.raises(Exception):
+        _hip.glu_interleave(qw[:96], rows[:96])

@@ -212,6 +212,22 @@ int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps, vo
   return ok();
 }
 
+int tvq_w8a8_gemm_glu(const int8_t* xq, const float* a_scales, const int8_t* qweight_glu, const float* w_scales_glu,
+                      void* y, int out_dtype, int64_t M, int64_t N2, int64_t K, void* stream) {
+  if (int rc = check_dtype(out_dtype)) return rc;
+  if (int rc = check_dims(M, N2, K)) return rc;
+  if (M == 0) return ok();
+  if (!xq || !a_scales || !qweight_glu || !w_scales_glu || !y) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (N2 % 64 != 0 || !dma_shape_ok(K))
+    return fail(TVQ_E_UNSUPPORTED, "gemm_glu needs N2 %% 64 == 0 and K %% 128 == 0 (K <= 2^22)");
+  if (!aligned16(xq) || !aligned16(qweight_glu) || !aligned16(y) || !aligned16(w_scales_glu))
+    return fail(TVQ_E_UNSUPPORTED, "gemm_glu needs 16-byte aligned pointers");
+  GemmArgs a{xq, a_scales, qweight_glu, w_scales_glu, nullptr, y, M, N2, K, true, out_dtype == TVQ_DTYPE_BF16, false};
+  hipError_t e = launch_dma_glu(a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "gemm_glu launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int tvq_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales, int dtype, int64_t M, int64_t I,
                  void* stream) {
   if (int rc = check_dtype(dtype)) return rc;

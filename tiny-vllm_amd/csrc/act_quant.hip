@@ -11,7 +11,7 @@
 //
 // One wave (64 lanes) owns one row; a 256-thread workgroup handles 4 rows.
 // HBM traffic is the algorithmic minimum for rows that fit the register
-// cache (K <= 64 * 8 * NI, NI = 1, 2, 4 or 8 by K, so short rows keep few
+// cache (K <= 64 * 8 * NI, NI = 1, 2, 4, 6 or 8 by K, so short rows keep few
 // VGPRs and many waves in flight): 2 B read + 1 B written per element and
 // 4 B per row. Longer rows are read a second time for the quantize pass
 // (that second read is served by L2). Codes take quant_code_fast; a vector
@@ -161,6 +161,7 @@ hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, floa
     if (K <= 512) TVQ_AQ(1);
     else if (K <= 1024) TVQ_AQ(2);
     else if (K <= 2048) TVQ_AQ(4);
+    else if (K <= 3072) TVQ_AQ(6);
     else TVQ_AQ(kMaxIters);
 #undef TVQ_AQ
   } else {

@@ -199,6 +199,20 @@ const char* dma_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t wo
   return dma_splits(w8a8, M, N, K, workspace_bytes) > 1 ? i.name_split : i.name;
 }
 
+// W8A8 gate_up with the SiLU-and-mul epilogue (gate/up rows interleaved in
+// 32-row blocks; y is [M, N/2]): the 256x256 tiles, whose wave tiles hold
+// one 32-column gate block and its up block.
+hipError_t launch_dma_glu(const GemmArgs& a, hipStream_t stream) {
+  constexpr CfgInfo i = info<DmaCfg::kI8_256x256>();
+  if (a.bf16)
+    return launch_dma<BF16, true, false, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false, false, true>(
+        a.x, a.a_scales, a.qweight, a.scales, nullptr, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0,
+        stream);
+  return launch_dma<F16, true, false, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false, false, true>(
+      a.x, a.a_scales, a.qweight, a.scales, nullptr, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0,
+      stream);
+}
+
 hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream) {
   if (a.w8a8) {
     if (a.raw_i32) return run<BF16, true, true>(a, stream);

@@ -223,7 +223,7 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false>
+          bool kNtW = false, bool kGlu = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
@@ -580,7 +580,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       // consecutive rows use different banks), then read it back
       // row-contiguous and store 16 bytes per lane: every row segment of the
       // slice leaves as whole 2*TN-byte runs.
-      constexpr int kRowB = 2 * C::TN;             // bytes per staged row
+      // kGlu: the weight rows come as 32-row blocks of gate and up channels
+      // (block 2b = gate channels 32b.., block 2b+1 = the matching up
+      // channels), so FN = 2 puts a gate column and its up column in the same
+      // lane; the slice stores round(silu(round(g)) * round(u)) into an
+      // output of N / 2 columns, exactly what the separate SiLU-and-mul
+      // kernel computes from the rounded gate_up output.
+      static_assert(!kGlu || (kW8A8 && MF == 32 && C::FN == 2), "GLU epilogue: W8A8, 32x32 tiles, FN = 2");
+      constexpr int kOutTN = kGlu ? C::TN / 2 : C::TN;  // output columns of the wave tile
+      const int n_out = kGlu ? N / 2 : N;
+      const int ncol_out = kGlu ? ncol0 / 2 : ncol0;
+      constexpr int kRowB = 2 * kOutTN;            // bytes per staged row
       constexpr int kCh = kRowB / 16;              // 16-byte chunks per row
       constexpr int kSwz = (kCh < 8 ? kCh : 8) - 1;
       constexpr int kRowsPer256 = kRowB >= 256 ? 1 : 256 / kRowB;
@@ -591,7 +601,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       const float* sc_w = sc + BM + wn * C::TN;
       const float* sc_b = sc + BM + BN + wn * C::TN;
       uint16_t* y = static_cast<uint16_t*>(yv);
-      const bool vec = (N & 7) == 0;
+      const bool vec = (n_out & 7) == 0;
       // Per-channel scales of this lane's columns, read once for all row
       // slices (LDS reads of the scales were a large share of the epilogue);
       // the bias, when there is one, is read per use.
@@ -608,6 +618,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
           const int mrow0 = m0 + wm * C::TM + MF * j;  // first output row of this slice
           float as = 0.0f;
           if constexpr (kW8A8) as = sc[wm * C::TM + MF * j + r];
+          if constexpr (kGlu) {
+#pragma unroll
+            for (int q = 0; q < kQ; ++q) {
+              const int nl = 8 * q + 4 * g;  // output column within the wave tile
+              float o[4];
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                const float gt = to_float<T>(from_float<T>(epi_w8a8_nb(acc[0][j][4 * q + t], as, wsv[0][q][t])));
+                const float ut = to_float<T>(from_float<T>(epi_w8a8_nb(acc[1][j][4 * q + t], as, wsv[1][q][t])));
+                o[t] = silu_f(gt) * ut;
+              }
+              u32x2 pk;
+              pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
+              pk.y = (uint32_t)from_float<T>(o[2]) | ((uint32_t)from_float<T>(o[3]) << 16);
+              *reinterpret_cast<u32x2*>(stg + r * kRowB + 16 * ((nl >> 3) ^ sswz(r)) + 2 * (nl & 7)) = pk;
+            }
+          } else
 #pragma unroll
           for (int i = 0; i < C::FN; ++i) {
 #pragma unroll
@@ -641,15 +668,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
             const int ch = e % kCh;
             const u32x4 val = *reinterpret_cast<const u32x4*>(stg + row * kRowB + 16 * (ch ^ sswz(row)));
             const int mo = mrow0 + row;
-            const int no = ncol0 + 8 * ch;
-            if (mo < M && no < N) {
-              uint16_t* dst = y + (int64_t)mo * N + no;
-              if (vec && no + 8 <= N) {
+            const int no = ncol_out + 8 * ch;
+            if (mo < M && no < n_out) {
+              uint16_t* dst = y + (int64_t)mo * n_out + no;
+              if (vec && no + 8 <= n_out) {
                 *reinterpret_cast<u32x4*>(dst) = val;
               } else {
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
-                  if (no + t < N) dst[t] = (uint16_t)(val[t >> 1] >> (16 * (t & 1)));
+                  if (no + t < n_out) dst[t] = (uint16_t)(val[t >> 1] >> (16 * (t & 1)));
               }
             }
           }
@@ -702,12 +729,12 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false>
+          bool kNtW = false, bool kGlu = false>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
                       int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
                       hipStream_t stream) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
-  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

@@ -101,13 +101,6 @@ __device__ __forceinline__ void quant_store(const u32x4 (&y)[NI], int nvec, int 
   }
 }
 
-// SiLU(a) = a / (1 + exp(-a)) = a * rcp(1 + 2^(-a log2 e)), on the hardware
-// exp2 and reciprocal (about 1 ulp each in fp32; the bf16/fp16 result is
-// then rounded once, as the reference's fused elementwise kernel rounds).
-__device__ __forceinline__ float silu_f(float a) {
-  return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
-}
-
 template <typename T, bool kRes, bool kY, bool kQ, int NI>
 __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
                                                           const uint16_t* __restrict__ w, float eps,

@@ -160,6 +160,13 @@ __device__ __forceinline__ float quant_code(float x, float s, float rs) {
   return fminf(fmaxf(t, -127.0f), 127.0f);
 }
 
+// SiLU(a) = a / (1 + exp(-a)) = a * rcp(1 + 2^(-a log2 e)), on the hardware
+// exp2 and reciprocal (about 1 ulp each in fp32; the bf16/fp16 result is
+// then rounded once, as the reference's fused elementwise kernel rounds).
+__device__ __forceinline__ float silu_f(float a) {
+  return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
+}
+
 // quant_code without its rare branch: rint(x * rs) clamped, and `near` set
 // when x * rs lies within 2^-14 of a half-integer. Callers OR `near` over a
 // wave (ballot) and redo those vectors with quant_code, so the common path

@@ -58,6 +58,7 @@ hipError_t launch_skinny(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_tiled(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_generic(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_dma_glu(const GemmArgs& a, hipStream_t stream);
 bool dma_shape_ok(int64_t K);
 // Path name, with a "_splitk" suffix when a workspace of the given size makes
 // the launch split K (which needs the device: without one it never splits).

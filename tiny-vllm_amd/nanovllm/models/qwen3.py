@@ -29,6 +29,8 @@ from nanovllm.layers.activation import SiluAndMul
 from nanovllm.layers.layernorm import RMSNorm
 from nanovllm.layers.linear import MergedColumnParallelLinear, QKVParallelLinear, RowParallelLinear
 from nanovllm.quantization import _hip
+from nanovllm.quantization.activation import QuantizedActivation
+from nanovllm.quantization.cuda import _get_w8a8_backend_preference
 from nanovllm.utils.context import get_context
 
 
@@ -195,8 +197,28 @@ class Qwen3MLP(nn.Module):
         self.act_fn = SiluAndMul()
         self.fuse_quant = quantization == "w8a8"
 
+    # W8A8 prefill: at this many tokens the gate_up GEMM runs its 256x256
+    # tiles anyway, and the SiLU-and-mul moves into its epilogue (the [M, 2I]
+    # gate_up output never reaches HBM; the result is bit-identical).
+    GLU_MIN_TOKENS = 4096
+
     def forward(self, x) -> torch.Tensor:
+        if (self.fuse_quant and isinstance(x, QuantizedActivation) and x.is_cuda and
+                x.xq.shape[0] >= self.GLU_MIN_TOKENS and _get_w8a8_backend_preference() == "native"):
+            return self.down_proj(self._glu_quant(x))
         return self.down_proj(self.act_fn(self.gate_up_proj(x), quant=self.fuse_quant))
+
+    def _glu_quant(self, x: "QuantizedActivation") -> "QuantizedActivation":
+        lin = self.gate_up_proj
+        cache = getattr(self, "_glu_weights", None)
+        if cache is None or cache[0] is not lin.qweight:
+            # gate/up rows regrouped once per weight tensor (an extra copy of
+            # gate_up's weights; the decode path keeps the original layout)
+            cache = (lin.qweight, *_hip.glu_interleave(lin.qweight.data, lin.w_scales.data))
+            self._glu_weights = cache
+        h = _hip.w8a8_gemm_glu(x.xq, x.scales, cache[1], cache[2], out_dtype=x.dtype)
+        q, s = _hip.act_quant(h)
+        return QuantizedActivation(q, s, x.dtype, (*x.shape[:-1], h.shape[-1]))
 
 
 class Qwen3DecoderLayer(nn.Module):

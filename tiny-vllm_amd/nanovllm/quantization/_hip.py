@@ -44,6 +44,7 @@ SYMBOLS = (
     ("tvq_gemm_workspace_bytes", _I64, ()),
     ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
+    ("tvq_w8a8_gemm_glu", _INT, (_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP)),
     ("tvq_qk_norm_rope", _INT, (_VP, _I64, _VP, _VP, _VP, _VP, _VP, ctypes.c_float, _I64, _INT, _INT, _INT, _I64,
                                 _VP, _VP, _VP, _VP, _VP, _I64, _I64, _INT, _VP)),
     ("tvq_prefill_attention", _INT, (_VP, _VP, _VP, _I64, _VP, _I64, _INT, _INT, _INT, ctypes.c_float, _VP, _INT,
@@ -237,6 +238,43 @@ def w8a8_gemm(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.Tensor, 
                                _ptr(bias), y.data_ptr(), _TORCH_TO_TVQ[out_dtype], m, n, k, *_ws(dev, split_k),
                                _stream(dev))
     _check(rc, "tvq_w8a8_gemm")
+    return y
+
+
+GLU_BLOCK = 32  # rows per gate / up block of tvq_w8a8_gemm_glu's weight layout
+
+
+def glu_interleave(qweight: torch.Tensor, w_scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Regroup gate_up rows [gate (I) ; up (I)] into 32-row blocks gate_b, up_b
+    (new row 64b + 32h + k <- old row h*I + 32b + k), the weight layout of
+    w8a8_gemm_glu. I must be a multiple of 32."""
+    n2 = qweight.shape[0]
+    _require(n2 % (2 * GLU_BLOCK) == 0, "gate_up rows must be a multiple of 64")
+    idx = torch.arange(n2, device=qweight.device).view(2, n2 // (2 * GLU_BLOCK), GLU_BLOCK).transpose(0, 1).reshape(-1)
+    return qweight.index_select(0, idx).contiguous(), w_scales.index_select(0, idx).contiguous()
+
+
+def w8a8_gemm_glu(x_q: torch.Tensor, a_scales: torch.Tensor, qweight_glu: torch.Tensor, w_scales_glu: torch.Tensor,
+                  out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """silu(gate) * up of the W8A8 gate_up projection, [M, I], with the
+    weights in glu_interleave layout; bit-identical to w8a8_gemm followed by
+    silu_mul."""
+    lib = load_library()
+    dev = _require_gpu(x_q, a_scales, qweight_glu, w_scales_glu)
+    _require(out_dtype in _TORCH_TO_TVQ, "out_dtype must be float16 or bfloat16")
+    _require(x_q.dim() == 2 and x_q.dtype == torch.int8 and x_q.is_contiguous(), "x_q must be a contiguous 2-D int8 tensor")
+    m, k = x_q.shape
+    _require(a_scales.dim() == 1 and a_scales.dtype == torch.float32 and a_scales.numel() == m,
+             "a_scales must be 1D float32 with one value per input row")
+    n2 = _check_weight(qweight_glu, w_scales_glu, None, k, out_dtype)
+    y = torch.empty((m, n2 // 2), dtype=out_dtype, device=dev)
+    if m == 0:
+        return y
+    with torch.cuda.device(dev):
+        rc = lib.tvq_w8a8_gemm_glu(x_q.data_ptr(), a_scales.data_ptr(), qweight_glu.data_ptr(),
+                                   w_scales_glu.data_ptr(), y.data_ptr(), _TORCH_TO_TVQ[out_dtype], m, n2, k,
+                                   _stream(dev))
+    _check(rc, "tvq_w8a8_gemm_glu")
     return y
 
 
