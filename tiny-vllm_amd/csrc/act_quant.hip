@@ -79,8 +79,11 @@ __device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs) {
 }
 
 // Vector path: K % 8 == 0 and 16-byte aligned x, 8-byte aligned xq.
+// NI >= 6: the compiler, left alone, took 129 (NI = 6) and 241 (NI = 8)
+// VGPRs for what fits in ~60; asking for 6 waves per SIMD keeps them at
+// 57 / 67 without spills (NI = 6 at 16384 x 3072: ~1.3 % of a W8A8 prefill).
 template <typename T, int NI>
-__global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NI >= 6 ? 6 : 1))) void act_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                             float eps, int8_t* __restrict__ xq,
                                                             float* __restrict__ a_scales) {
   const int lane = threadIdx.x & 63;
