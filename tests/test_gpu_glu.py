@@ -42,3 +42,38 @@ def test_gemm_glu_matches_gemm_then_silu_mul(hiplib, m, i, k, dtype):
 def test_gemm_glu_back_to_back_calls_with_smaller_input(hiplib):
     _case(4096, 3072, 1024, torch.bfloat16, seed=1)
     _case(257, 3072, 1024, torch.bfloat16, seed=2)
+
+
+def test_mlp_glu_path_matches_unfused_and_follows_weight_updates(hiplib):
+    """The engine MLP at >= GLU_MIN_TOKENS tokens (fused gate_up + SiLU-and-mul)
+    equals the unfused path, also after the weights change in place."""
+    from nanovllm.models.qwen3 import Qwen3Config, Qwen3MLP
+    from nanovllm.quantization import _hip
+    from nanovllm.quantization.activation import QuantizedActivation
+    print("CASE mlp glu path", flush=True)
+    cfg = Qwen3Config(hidden_size=256, intermediate_size=512)
+    mlp = Qwen3MLP(cfg, "w8a8").cuda()
+    g = torch.Generator().manual_seed(7)
+
+    def draw():
+        for lin in (mlp.gate_up_proj, mlp.down_proj):
+            q, s = quantize_int8_per_channel(torch.randn(lin.qweight.shape, generator=g) * 0.02)
+            lin.qweight.copy_(q.cuda())
+            lin.w_scales.copy_(s.float().cuda())
+
+    def unfused(qa):
+        keep = Qwen3MLP.GLU_MIN_TOKENS
+        Qwen3MLP.GLU_MIN_TOKENS = 1 << 40
+        try:
+            return mlp(qa)
+        finally:
+            Qwen3MLP.GLU_MIN_TOKENS = keep
+
+    m = Qwen3MLP.GLU_MIN_TOKENS
+    xq, xs = _hip.act_quant(make_activations(m, 256, seed=3).cuda())
+    qa = QuantizedActivation(xq, xs, torch.bfloat16, (m, 256))
+    with torch.no_grad():
+        draw()
+        assert torch.equal(mlp(qa), unfused(qa))
+        draw()  # in place: the regrouped copy must follow
+        assert torch.equal(mlp(qa), unfused(qa))

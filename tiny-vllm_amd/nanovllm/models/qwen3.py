@@ -210,11 +210,14 @@ class Qwen3MLP(nn.Module):
 
     def _glu_quant(self, x: "QuantizedActivation") -> "QuantizedActivation":
         lin = self.gate_up_proj
+        # gate/up rows regrouped once per weight state (an extra copy of
+        # gate_up's weights; the decode path keeps the original layout). The
+        # key follows in-place updates (copy_ bumps _version) and re-allocation;
+        # load_weights also drops the copy.
+        key = (lin.qweight.data_ptr(), lin.qweight._version, lin.w_scales.data_ptr(), lin.w_scales._version)
         cache = getattr(self, "_glu_weights", None)
-        if cache is None or cache[0] is not lin.qweight:
-            # gate/up rows regrouped once per weight tensor (an extra copy of
-            # gate_up's weights; the decode path keeps the original layout)
-            cache = (lin.qweight, *_hip.glu_interleave(lin.qweight.data, lin.w_scales.data))
+        if cache is None or cache[0] != key:
+            cache = (key, *_hip.glu_interleave(lin.qweight.data, lin.w_scales.data))
             self._glu_weights = cache
         h = _hip.w8a8_gemm_glu(x.xq, x.scales, cache[1], cache[2], out_dtype=x.dtype)
         q, s = _hip.act_quant(h)

@@ -70,3 +70,8 @@ def load_model(model: nn.Module, path: str, quantization: str | None = None) -> 
         _validate_quantized_loaded(model, loaded, ".scales", "INT8")
     elif quantization == "w8a8":
         _validate_quantized_loaded(model, loaded, ".w_scales", "W8A8")
+    # derived weight copies (the MLP's regrouped gate_up for the fused
+    # SiLU-and-mul GEMM) are rebuilt from the new weights on next use
+    for mod in model.modules():
+        if hasattr(mod, "_glu_weights"):
+            del mod._glu_weights
