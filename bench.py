@@ -34,6 +34,9 @@ for _p in (str(ROOT), str(ROOT / "tiny-vllm_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
+# Native failures must raise, never be served by the torch path.
+os.environ["NANOVLLM_NATIVE_STRICT"] = "1"
+
 import torch  # noqa: E402
 
 METRIC = "int8 GEMM TOPS & HBM GB/s (% roofline) at decode/prefill M; decode tok/s"

@@ -15,6 +15,7 @@ force on tiny inputs and against invariants.
 Parity status per function (see tests/test_oracle.py):
   quantize_rows            pinned (closed forms, ties, zero rows, torch, C)
   gemm_i32                 pinned (brute force, C vs numpy, invariants)
+  gemm_i32_blas            pinned (equal to gemm_i32 / C at +-127 extremes)
   w8a8_epilogue_bf16       pinned (fp64 bound, sign/zero cases, C vs numpy)
   w8a16_torch_path         pinned against the exact fp64 product (bound)
   w8a8_torch_path          pinned against the exact fp64 product (bound)
@@ -81,6 +82,16 @@ def quantize_rows(x_f32: np.ndarray, eps: np.float32 = EPS) -> tuple[np.ndarray,
 def gemm_i32(xq: np.ndarray, w: np.ndarray) -> np.ndarray:
     """Exact accumulator sum_k xq[m,k]*w[n,k] (w8a8_gemm.cu:336-375), via int64."""
     acc = xq.astype(np.int64) @ w.astype(np.int64).T
+    assert np.abs(acc).max(initial=0) < 2**31
+    return acc.astype(np.int32)
+
+
+def gemm_i32_blas(xq: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """The same exact accumulator through a float64 BLAS product, for shapes
+    too large for the scalar loops: every product is an integer of magnitude
+    <= 127*127 and every partial sum stays below 2**31 << 2**53, so each
+    float64 addition is exact whatever order the BLAS sums in."""
+    acc = np.asarray(xq, np.float64) @ np.asarray(w, np.float64).T
     assert np.abs(acc).max(initial=0) < 2**31
     return acc.astype(np.int32)
 

@@ -4,6 +4,10 @@ from pathlib import Path
 
 import pytest
 
+# Native failures raise instead of falling back to the torch path, so no parity
+# check can pass on the fallback.
+os.environ.setdefault("NANOVLLM_NATIVE_STRICT", "1")
+
 ROOT = Path(__file__).resolve().parents[1]
 PKG = ROOT / "tiny-vllm_amd"
 for p in (str(ROOT), str(PKG)):

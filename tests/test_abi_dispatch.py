@@ -192,14 +192,11 @@ def test_forced_fallback_logs_reason(monkeypatch, capsys):
     monkeypatch.setenv("NANOVLLM_INT8_BACKEND", "fallback")
     monkeypatch.setenv("NANOVLLM_INT8_LOG_PATH", "1")
     cuda._LOGGED_KERNEL_EVENTS.clear()
-    from nanovllm.utils.context import reset_context, set_context
-    set_context(True)
-    try:
+    from nanovllm.utils.context import step_context
+    with step_context(True):
         lay, x, q, s = _cpu_layer(__import__("nanovllm.quantization", fromlist=["x"]).Int8WeightOnlyQuantMethod(),
                                   32, 64)
         cuda.apply_int8_weight_only_linear(x, lay.qweight, lay.scales)
-    finally:
-        reset_context()
     line = capsys.readouterr().out.strip()
     assert "backend=fallback phase=prefill path=python_fallback" in line
     assert line.endswith("reason=backend_forced_fallback")
@@ -273,3 +270,65 @@ def test_glu_interleave_layout():
     assert torch.equal(q2, qw[s2.long()])
     with pytest.raises(Exception):
         _hip.glu_interleave(qw[:96], rows[:96])
+
+
+def _pretend_native(monkeypatch, cuda):
+    """Route CPU tensors into the native branch, whose call then raises."""
+    monkeypatch.setattr(cuda, "_on_gpu", lambda *t: True)
+    monkeypatch.setattr(cuda._hip, "load_library", lambda: None)
+
+    def boom(*a, **k):
+        raise RuntimeError("tvq_w8a16_gemm failed (code -2): unsupported")
+    monkeypatch.setattr(cuda, "native_int8_weight_only_linear", boom)
+    monkeypatch.setattr(cuda, "native_w8a8_linear", boom)
+
+
+def test_native_failure_falls_back_like_reference(monkeypatch, capsys):
+    """Default dispatch (reference cuda.py:344-356, 487-503): a native failure is
+    logged once as native_unavailable and the torch path computes the result."""
+    from nanovllm.quantization import cuda, Int8WeightOnlyQuantMethod
+    monkeypatch.delenv("NANOVLLM_NATIVE_STRICT", raising=False)
+    monkeypatch.setenv("NANOVLLM_INT8_LOG_PATH", "1")
+    monkeypatch.setenv("NANOVLLM_W8A8_LOG_PATH", "1")
+    monkeypatch.setenv("NANOVLLM_INT8_BACKEND", "native")
+    monkeypatch.setenv("NANOVLLM_W8A8_BACKEND", "native")
+    cuda._LOGGED_KERNEL_EVENTS.clear()
+    _pretend_native(monkeypatch, cuda)
+    lay, x, q, s = _cpu_layer(Int8WeightOnlyQuantMethod(), 32, 64)
+    y = cuda.apply_int8_weight_only_linear(x, q, s)
+    assert torch.equal(y, cuda.int8_weight_only_linear_fallback(x, q, s))
+    xq, a_s = oracle.quantize_rows_torch(x.reshape(-1, 64))
+    y8 = cuda.apply_w8a8_linear(xq, a_s, q, s, None, torch.bfloat16)
+    assert torch.equal(y8, cuda.w8a8_linear_fallback(xq, a_s, q, s, None, torch.bfloat16))
+    out = capsys.readouterr().out.strip().splitlines()
+    assert len(out) == 2
+    assert all("backend=fallback" in l and "path=python_fallback" in l for l in out)
+    assert all("reason=native_unavailable RuntimeError: tvq_w8a16_gemm failed" in l for l in out)
+
+
+def test_strict_switch_reraises_native_failure(monkeypatch):
+    """NANOVLLM_NATIVE_STRICT=1 (set by tests, smoke and bench) re-raises."""
+    from nanovllm.quantization import cuda, Int8WeightOnlyQuantMethod
+    monkeypatch.setenv("NANOVLLM_NATIVE_STRICT", "1")
+    monkeypatch.setenv("NANOVLLM_INT8_BACKEND", "native")
+    monkeypatch.setenv("NANOVLLM_W8A8_BACKEND", "native")
+    _pretend_native(monkeypatch, cuda)
+    lay, x, q, s = _cpu_layer(Int8WeightOnlyQuantMethod(), 32, 64)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        cuda.apply_int8_weight_only_linear(x, q, s)
+    xq, a_s = oracle.quantize_rows_torch(x.reshape(-1, 64))
+    with pytest.raises(RuntimeError, match="unsupported"):
+        cuda.apply_w8a8_linear(xq, a_s, q, s, None, torch.bfloat16)
+
+
+def test_missing_library_is_never_hidden(monkeypatch):
+    """A missing HIP library raises even without the strict switch."""
+    from nanovllm.quantization import cuda, Int8WeightOnlyQuantMethod
+    monkeypatch.delenv("NANOVLLM_NATIVE_STRICT", raising=False)
+    monkeypatch.setenv("NANOVLLM_INT8_BACKEND", "native")
+    monkeypatch.setattr(cuda, "_on_gpu", lambda *t: True)
+    monkeypatch.setattr(cuda._hip, "_LIB", None)
+    monkeypatch.setenv("TVQ_LIBRARY", "/nonexistent/libtinyvllm_quant.so")
+    lay, x, q, s = _cpu_layer(Int8WeightOnlyQuantMethod(), 32, 64)
+    with pytest.raises(RuntimeError, match="not found"):
+        cuda.apply_int8_weight_only_linear(x, q, s)

@@ -18,7 +18,7 @@ from nanovllm.engine.model_runner import random_init_
 from nanovllm.engine.scheduler import Scheduler
 from nanovllm.engine.sequence import Sequence, SequenceStatus
 from nanovllm.models.qwen3 import Qwen3Config
-from nanovllm.utils.context import set_context
+from nanovllm.utils.context import step_context
 
 TINY = dict(vocab_size=256, hidden_size=64, intermediate_size=128, num_hidden_layers=2, num_attention_heads=4,
             num_key_value_heads=2, head_dim=16, max_position_embeddings=256)
@@ -98,8 +98,7 @@ def test_kv_cache_decode_matches_recompute():
     distinct = 0
     for p, o in zip(prompts, outs):
         full = p + o["token_ids"]
-        set_context(True, cu_seqlens_q=torch.tensor([0, len(full)]), slot_mapping=None)
-        with torch.no_grad():
+        with torch.no_grad(), step_context(True, cu_seqlens_q=torch.tensor([0, len(full)])):
             logits = model.compute_logits(model(torch.tensor(full), torch.arange(len(full))))
         pred = logits[len(p) - 1: len(full) - 1].float()
         top2 = pred.topk(2, dim=-1).values
@@ -170,3 +169,62 @@ def test_engine_loads_checkpoint_and_quantized_artifact(tmp_path, mode):
     a = [o["token_ids"] for o in ref.generate(prompts, sp, use_tqdm=False)]
     b = [o["token_ids"] for o in q.generate(prompts, sp, use_tqdm=False)]
     assert a[0][0] == b[0][0] and a[1][0] == b[1][0]  # first tokens agree under int8 weights
+
+
+def test_glu_cache_key_follows_every_kind_of_weight_change():
+    """The fused gate_up path's regrouped-weight cache key changes on in-place
+    updates, on loader writes through .data and on re-assignment."""
+    from nanovllm.models.qwen3 import Qwen3MLP
+    mlp = Qwen3MLP(Qwen3Config(hidden_size=256, intermediate_size=512), "w8a8")
+    lin = mlp.gate_up_proj
+    keys = [mlp._glu_key()]
+    with torch.no_grad():
+        lin.qweight.copy_(torch.ones_like(lin.qweight))
+    keys.append(mlp._glu_key())
+    lin.qweight.weight_loader(lin.qweight, torch.zeros_like(lin.qweight))
+    keys.append(mlp._glu_key())
+    lin.w_scales.weight_loader(lin.w_scales, torch.ones(lin.w_scales.shape))
+    keys.append(mlp._glu_key())
+    lin.qweight = torch.nn.Parameter(torch.zeros_like(lin.qweight), requires_grad=False)
+    keys.append(mlp._glu_key())
+    assert len(set(keys)) == len(keys)
+
+
+def test_glu_fused_path_shape_gate():
+    from nanovllm.models.qwen3 import Qwen3MLP
+    assert Qwen3MLP(Qwen3Config(hidden_size=1024, intermediate_size=3072), "w8a8").glu_shape_ok()
+    assert not Qwen3MLP(Qwen3Config(hidden_size=1000, intermediate_size=3072), "w8a8").glu_shape_ok()
+    assert not Qwen3MLP(Qwen3Config(hidden_size=1024, intermediate_size=3000), "w8a8").glu_shape_ok()
+
+
+def test_step_context_nesting_and_validation():
+    from nanovllm.utils.context import get_context, step_context
+    assert not get_context().is_prefill
+    with step_context(True, max_seqlen_q=7) as outer:
+        assert get_context() is outer
+        with step_context(False, context_lens=torch.ones(2)):
+            assert not get_context().is_prefill
+        assert get_context() is outer
+    assert not get_context().is_prefill and get_context().max_seqlen_q == 0
+    with pytest.raises(TypeError, match="do not belong to a prefill"):
+        with step_context(True, context_lens=torch.ones(2)):
+            pass
+    with pytest.raises(TypeError, match="unknown step metadata"):
+        with step_context(False, bogus=1):
+            pass
+    with pytest.raises(RuntimeError):
+        with step_context(True):
+            raise RuntimeError("inside")
+    assert not get_context().is_prefill
+
+
+def test_sequence_keeps_prompt_and_output_apart():
+    s = Sequence([4, 5, 6], SamplingParams(max_tokens=3))
+    assert len(s) == 3 and s.last_token == 6 and s.num_completion_tokens == 0
+    s.append_token(9)
+    assert s.token_ids == [4, 5, 6, 9] and s.completion_token_ids == [9] and s.last_token == 9
+    assert s.num_prompt_tokens == 3 and len(s) == 4 and s.max_tokens == 3
+    t = Sequence([1])
+    assert t.seq_id > s.seq_id
+    with pytest.raises(ValueError):
+        Sequence([])

@@ -21,16 +21,20 @@ from nanovllm import LLM, SamplingParams
 from nanovllm.engine.model_runner import random_init_
 from nanovllm.models.qwen3 import Qwen3Config
 from nanovllm.quantization import _hip
-from nanovllm.utils.context import set_context
+from nanovllm.utils.context import step_context
 
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(vocab_size=1024, hidden_size=256, intermediate_size=768, num_hidden_layers=3, num_attention_heads=4,
              num_key_value_heads=2, head_dim=128, max_position_embeddings=512)
+# The real Qwen3-0.6B architecture: 28 layers, hidden 1024,
+# intermediate 3072, 16 q / 8 kv heads, head_dim 128, vocab 151936.
+QWEN3_06B = dict(vocab_size=151936, hidden_size=1024, intermediate_size=3072, num_hidden_layers=28,
+                 num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=4096)
 
 
-def _engine(quantization, device="cuda", std=0.08, eager=True):
-    llm = LLM(Qwen3Config(**SMALL), device=device, quantization=quantization, max_model_len=256,
+def _engine(quantization, device="cuda", std=0.08, eager=True, arch=SMALL):
+    llm = LLM(Qwen3Config(**arch), device=device, quantization=quantization, max_model_len=256,
               max_num_batched_tokens=512, max_num_seqs=8, enforce_eager=eager)
     random_init_(llm.model_runner.model, seed=3, std=std, device=device)
     return llm
@@ -40,11 +44,10 @@ def _prefill_logits(model, ids: list[int], device) -> torch.Tensor:
     """Cache-free prefill of one sequence (no KV slot written)."""
     n = len(ids)
     if device == "cuda":
-        set_context(True, cu_seqlens_q=torch.tensor([0, n]), max_seqlen_q=n, slot_mapping=None,
-                    attn_blocks=_hip.prefill_blocks([(0, n)]).cuda())
+        meta = dict(attn_blocks=_hip.prefill_blocks([(0, n)]).cuda())
     else:
-        set_context(True, cu_seqlens_q=torch.tensor([0, n]), slot_mapping=None)
-    with torch.no_grad():
+        meta = {}
+    with torch.no_grad(), step_context(True, cu_seqlens_q=torch.tensor([0, n]), max_seqlen_q=n, **meta):
         x = torch.tensor(ids, device=device)
         return model.compute_logits(model(x, torch.arange(len(ids), device=device))).float().cpu()
 
@@ -67,18 +70,17 @@ def test_quantized_projections_run_native(gpu, hiplib, monkeypatch, mode):
             return orig(*a, **k)
         return counted
 
+    llm = _engine(mode)  # its warm-up prefill runs before the counting starts
     for name in names:
         monkeypatch.setattr(_hip, name, counting(getattr(_hip, name)))
-    llm = _engine(mode)
     llm.generate([[1, 2, 3, 4, 5, 6]], SamplingParams(temperature=0.0, max_tokens=3, ignore_eos=True),
                  use_tqdm=False)
     # 1 prefill + 2 decode steps, 4 projections x 3 layers each
     assert calls["n"] == 3 * 4 * 3
 
 
-@pytest.mark.parametrize("mode", ["int8", "w8a8"])
-def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
-    """Every quantized projection of a GPU forward, on the activations it
+def _check_projections_against_oracle(llm, mode, arch, prompt):
+    """Every quantized projection of one GPU prefill, on the activations it
     actually received, against the oracle on those same activations: the
     act-quant codes and scales are bit-exact, the outputs within the bf16
     tolerance of the reference's torch path and of the kernels' own
@@ -86,9 +88,9 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
     import oracle
     from nanovllm.layers.linear import LinearBase
     from nanovllm.quantization.activation import QuantizedActivation
-    llm = _engine(mode)
     model = llm.model_runner.model
     seen = []
+
     def grab(mod, inp, out):
         x = inp[0]
         x = QuantizedActivation(x.xq.cpu(), x.scales.cpu(), x.dtype, x.shape) \
@@ -96,10 +98,11 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
         seen.append((mod, x, out.detach().cpu()))
 
     hooks = [m.register_forward_hook(grab) for m in model.modules() if isinstance(m, LinearBase)]
-    _prefill_logits(model, list(range(7, 7 + 200, 3)) + [5] * 31, "cuda")
+    _prefill_logits(model, prompt, "cuda")
     for h in hooks:
         h.remove()
-    assert len(seen) == 4 * SMALL["num_hidden_layers"]
+    layers = arch["num_hidden_layers"]
+    assert len(seen) == 4 * layers
     fused = 0
     for mod, x, y in seen:
         q = mod.qweight.cpu()
@@ -125,7 +128,38 @@ def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
             assert oracle.max_abs_ratio(yf, rf) <= oracle.MAX_ABS_TOL
         # against its own numerics the kernel is far tighter than the tolerance
         assert oracle.rel_l2(yf, ref_own.float().numpy()) < 2e-3
-    assert fused == (3 * SMALL["num_hidden_layers"] if mode == "w8a8" else 0)
+    assert fused == (3 * layers if mode == "w8a8" else 0)
+
+
+@pytest.mark.parametrize("mode", ["int8", "w8a8"])
+def test_projections_inside_model_match_oracle(gpu, hiplib, mode):
+    _check_projections_against_oracle(_engine(mode), mode, SMALL, list(range(7, 7 + 200, 3)) + [5] * 31)
+
+
+@pytest.mark.parametrize("mode", ["int8", "w8a8"])
+def test_qwen3_06b_architecture_projections_match_oracle(gpu, hiplib, mode):
+    """The full 28-layer Qwen3-0.6B architecture (random init): all 112
+    projections of a 2-prompt prefill against the oracle."""
+    print(f"CASE qwen3_06b projections mode={mode}", flush=True)
+    llm = _engine(mode, std=0.02, arch=QWEN3_06B)
+    _check_projections_against_oracle(llm, mode, QWEN3_06B, list(range(100, 100 + 7 * 60, 7)) + [9] * 37)
+
+
+@pytest.mark.parametrize("mode", [None, "int8", "w8a8"])
+def test_qwen3_06b_architecture_graph_decode_matches_eager(gpu, hiplib, mode):
+    """Qwen3-0.6B architecture: greedy decode through the captured HIP graphs
+    gives the same tokens as eager execution."""
+    print(f"CASE qwen3_06b graph-vs-eager mode={mode}", flush=True)
+    prompts = [list(range(1000, 1000 + 90)), [5, 17, 33, 2, 90, 41], [77] * 31]
+    sp = SamplingParams(temperature=0.0, max_tokens=10, ignore_eos=True)
+    outs = {}
+    for eager in (True, False):
+        llm = _engine(mode, std=0.02, eager=eager, arch=QWEN3_06B)
+        assert bool(llm.model_runner.graphs) == (not eager)
+        outs[eager] = [o["token_ids"] for o in llm.generate(prompts, sp, use_tqdm=False)]
+        del llm
+        torch.cuda.empty_cache()
+    assert outs[True] == outs[False]
 
 
 def test_bf16_kv_cache_decode_matches_recompute(gpu):

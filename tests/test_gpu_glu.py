@@ -77,3 +77,15 @@ def test_mlp_glu_path_matches_unfused_and_follows_weight_updates(hiplib):
         assert torch.equal(mlp(qa), unfused(qa))
         draw()  # in place: the regrouped copy must follow
         assert torch.equal(mlp(qa), unfused(qa))
+        # through the layer's weight_loader hooks (they write via .data, which
+        # does not advance _version): the copy must follow
+        lin = mlp.gate_up_proj
+        q, s = quantize_int8_per_channel(torch.randn(lin.qweight.shape, generator=g) * 0.02)
+        lin.qweight.weight_loader(lin.qweight, q)
+        lin.w_scales.weight_loader(lin.w_scales, s.float())
+        assert torch.equal(mlp(qa), unfused(qa))
+        # re-assigned parameters (new tensors, possibly at a reused address)
+        q, s = quantize_int8_per_channel(torch.randn(lin.qweight.shape, generator=g) * 0.02)
+        lin.qweight = torch.nn.Parameter(q.cuda(), requires_grad=False)
+        lin.w_scales = torch.nn.Parameter(s.float().cuda(), requires_grad=False)
+        assert torch.equal(mlp(qa), unfused(qa))

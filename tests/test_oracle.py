@@ -230,6 +230,31 @@ def test_w8a8_epilogue_zero_sign_and_order():
     assert yf[0, 3] == np.float32(np.float32(1.5) * np.float32(1.0 / 3.0))
 
 
+def test_w8a8_epilogue_order_known_answers():
+    """Vectors found by a CPU brute-force search where (acc*a_s)*w_s (the
+    reference order, w8a8_gemm.cu:387-389) and acc*(a_s*w_s) round to
+    different fp32 values and, for the first three, to different bf16 values.
+    The expected bits are those of the reference order."""
+    u = lambda v: np.array([v], np.uint32).view(np.float32)[0]
+    cases = [  # acc, a_s bits, w_s bits, fp32 result (ref order), bf16 bits (ref order, other order)
+        (589386, 1058899755, 972549179, 171.5, 17196, 17195),
+        (297063, 1035536272, 1005178573, 191.5, 17216, 17215),
+        (3299, 1058281226, 967378317, None, 16158, 16157),
+    ]
+    for acc_v, a_bits, w_bits, want_f, want_b, other_b in cases:
+        a_s, w_s = u(a_bits), u(w_bits)
+        yb, yf = oracle.c_w8a8_epilogue(np.array([[acc_v]], np.int32), np.array([a_s]), np.array([w_s]))
+        ref = np.float32(np.float32(np.float32(acc_v) * a_s) * w_s)
+        alt = np.float32(np.float32(acc_v) * np.float32(a_s * w_s))
+        assert ref != alt  # the vector does separate the two orders
+        assert yf[0, 0] == ref and yf[0, 0] != alt
+        if want_f is not None:
+            assert yf[0, 0] == np.float32(want_f)
+        assert yb[0, 0] == want_b and yb[0, 0] != other_b
+        # numpy restatement agrees
+        assert oracle.w8a8_epilogue_f32(np.array([[acc_v]], np.int32), np.array([a_s]), np.array([w_s]))[0, 0] == ref
+
+
 def test_w8a8_epilogue_bias_is_fused_fma():
     acc = np.array([[1 << 24 | 1]], np.int32)
     a_s = np.array([1.0], np.float32)
@@ -369,3 +394,19 @@ def test_golden_fixture(path):
         np.testing.assert_array_equal(s, d["s"])
     else:
         pytest.fail(f"unknown fixture kind {kind}")
+
+
+def test_gemm_i32_blas_exact():
+    """The float64-BLAS accumulator equals the integer loops bit for bit,
+    including all-extreme rows at the largest K (|acc| = 127*127*12288)."""
+    rng = np.random.default_rng(21)
+    for m, n, k in ((7, 33, 40), (64, 96, 4096), (5, 17, 12288)):
+        xq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+        w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+        xq[0] = 127
+        w[0] = -127
+        w[1] = 127
+        got = oracle.gemm_i32_blas(xq, w)
+        np.testing.assert_array_equal(got, oracle.c_gemm_i32(xq, w))
+        np.testing.assert_array_equal(got, oracle.gemm_i32(xq, w))
+        assert got[0, 0] == -127 * 127 * k and got[0, 1] == 127 * 127 * k

@@ -63,7 +63,8 @@ class LLMEngine:
     def step(self):
         seqs, is_prefill = self.scheduler.schedule()
         token_ids = self.model_runner.run(seqs, is_prefill)
-        num_tokens = sum(len(s) - s.num_cached_tokens for s in seqs) if is_prefill else -len(seqs)
+        # no prefix caching here: a prefill step computes every prompt token
+        num_tokens = sum(len(s) for s in seqs) if is_prefill else -len(seqs)
         self.scheduler.postprocess(seqs, token_ids)
         outputs = [(s.seq_id, s.completion_token_ids) for s in seqs if s.is_finished]
         return outputs, num_tokens

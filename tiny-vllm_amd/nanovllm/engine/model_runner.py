@@ -34,7 +34,7 @@ from nanovllm.layers.linear import LinearBase
 from nanovllm.models.qwen3 import Attention, Qwen3ForCausalLM, RMSNorm
 from nanovllm.quantization import _hip
 from nanovllm.quantization.utils import quantize_int8_per_channel
-from nanovllm.utils.context import reset_context, set_context
+from nanovllm.utils.context import step_context
 from nanovllm.utils.loader import load_model
 
 
@@ -102,18 +102,49 @@ class ModelRunner:
             # the split-K GEMM workspace must exist before any graph capture
             from nanovllm.quantization import _hip
             _hip.gemm_workspace(torch.device("cuda", 0))
+            self._warmup_model()
         self._allocate_kv_cache()
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         if device == "cuda" and not config.enforce_eager:
             self.capture_graphs()
+
+    @torch.no_grad()
+    def _warmup_model(self) -> None:
+        """One cache-free prefill of the largest batch the scheduler can form
+        (max_num_batched_tokens tokens in sequences of max_model_len), so the
+        KV cache is sized after the peak activation memory is known and after
+        the lazily built per-layer buffers (the regrouped gate_up weights of
+        the fused W8A8 MLP) exist. Mirrors warmup_model + the peak accounting
+        of the reference (model_runner.py:114-133)."""
+        cfg = self.config
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        seq_len = min(cfg.max_model_len, cfg.max_num_batched_tokens)
+        num = max(1, min(cfg.max_num_batched_tokens // seq_len, cfg.max_num_seqs))
+        total = num * seq_len
+        with step_context(True, cu_seqlens_q=torch.arange(0, total + 1, seq_len), max_seqlen_q=seq_len,
+                          attn_blocks=_hip.prefill_blocks([(i * seq_len, seq_len) for i in range(num)]).cuda()):
+            ids = torch.zeros(total, dtype=torch.int64, device="cuda")
+            pos = torch.arange(seq_len, device="cuda").repeat(num)
+            hidden = self.model(ids, pos)
+            self.model.compute_logits(hidden[seq_len - 1::seq_len])
+            torch.cuda.synchronize()
+        self.warmup_peak_bytes = torch.cuda.max_memory_allocated()
+        torch.cuda.empty_cache()
 
     def _allocate_kv_cache(self) -> None:
         cfg, hf = self.config, self.config.hf_config
         attns = [m for m in self.model.modules() if isinstance(m, Attention)]
         per_slot = 2 * len(attns) * attns[0].num_kv_heads * cfg.max_model_len * hf.head_dim * 2
         if self.device == "cuda":
-            free, _ = torch.cuda.mem_get_info()
-            budget = int(free * cfg.gpu_memory_utilization)
+            # the reference's accounting (model_runner.py:114-133): the share
+            # of total memory left after the warmup's peak, minus what other
+            # allocations outside torch already hold
+            free, total = torch.cuda.mem_get_info()
+            used = total - free
+            current = torch.cuda.memory_stats()["allocated_bytes.all.current"]
+            peak = max(self.warmup_peak_bytes, current)
+            budget = int(total * cfg.gpu_memory_utilization - used - peak + current)
         else:
             budget = 1 << 30
         self.num_slots = min(cfg.max_num_seqs, budget // per_slot)
@@ -142,15 +173,14 @@ class ModelRunner:
         pool = None
         for bs in reversed(self.graph_bs):
             graph = torch.cuda.CUDAGraph()
-            set_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs])
-            gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])  # warm-up
-            with torch.cuda.graph(graph, pool):
-                gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
+            with step_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs]):
+                gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])  # warm-up
+                with torch.cuda.graph(graph, pool):
+                    gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
             if pool is None:
                 pool = graph.pool()
             self.graphs[bs] = graph
             torch.cuda.synchronize()
-            reset_context()
         self.graph_vars = gv
 
     def _replay_decode(self, seqs: list[Sequence]) -> torch.Tensor:
@@ -177,43 +207,46 @@ class ModelRunner:
     @torch.no_grad()
     def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
         if is_prefill:
-            # Per-token inputs are built with array ops: only the token ids
-            # cross from Python (one fromiter); positions and per-token slots
-            # expand from the per-sequence lengths on the device. The list
-            # loops they replace cost ~5 ms of host time per 16k tokens,
-            # during which the GPU had nothing queued.
-            lens = [len(s) for s in seqs]
-            cu = [0, *itertools.accumulate(lens)]
-            total = cu[-1]
-            ids = torch.from_numpy(np.fromiter(itertools.chain.from_iterable(s.token_ids for s in seqs),
-                                               dtype=np.int64, count=total))
-            lmax = max(lens)
-            lens_t = self._to_gpu(lens, torch.int64)
-            starts = self._to_gpu(cu[:-1], torch.int64)
-            pos = torch.arange(total, device=lens_t.device) - torch.repeat_interleave(starts, lens_t, output_size=total)
-            if self.device == "cuda":
-                blocks = _hip.prefill_blocks([(cu[i], n) for i, n in enumerate(lens)])
-                slots = self._to_gpu([s.slot for s in seqs], torch.int64)
-                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax, slot_mapping=slots,
-                            attn_blocks=blocks.pin_memory().cuda(non_blocking=True),
-                            token_slots=torch.repeat_interleave(slots, lens_t, output_size=total))
-                ids = ids.pin_memory().cuda(non_blocking=True)
-            else:
-                set_context(True, cu_seqlens_q=torch.tensor(cu), max_seqlen_q=lmax,
-                            slot_mapping=torch.tensor([s.slot for s in seqs]))
-            hidden = self.model(ids, pos)
-            hidden = hidden[self._to_gpu(cu[1:], torch.int64) - 1]
+            hidden = self._prefill(seqs)
         elif self.graphs and len(seqs) <= self.graph_bs[-1]:
-            hidden = self._replay_decode(seqs)
+            with step_context(False):
+                hidden = self._replay_decode(seqs)
         else:
             slots = [s.slot for s in seqs]
             lens = [len(s) for s in seqs]
-            set_context(False, max_seqlen_k=max(lens), slot_mapping=self._to_gpu(slots, torch.int32),
-                        context_lens=self._to_gpu(lens, torch.int32), kv_lo=min(slots), kv_hi=max(slots) + 1)
-            hidden = self.model(self._to_gpu([s.last_token for s in seqs], torch.int64),
-                                self._to_gpu([n - 1 for n in lens], torch.int64))
+            with step_context(False, max_seqlen_k=max(lens), slot_mapping=self._to_gpu(slots, torch.int32),
+                              context_lens=self._to_gpu(lens, torch.int32), kv_lo=min(slots), kv_hi=max(slots) + 1):
+                hidden = self.model(self._to_gpu([s.last_token for s in seqs], torch.int64),
+                                    self._to_gpu([n - 1 for n in lens], torch.int64))
         logits = self.model.compute_logits(hidden)
         temps = self._to_gpu([s.temperature for s in seqs], torch.float32)
-        tokens = sample(logits, temps).tolist()
-        reset_context()
-        return tokens
+        return sample(logits, temps).tolist()
+
+    def _prefill(self, seqs: list[Sequence]) -> torch.Tensor:
+        """Forward of the packed prompts; returns each sequence's last hidden row.
+
+        Per-token inputs are built with array ops: only the token ids cross
+        from Python (one fromiter); positions and per-token slots expand from
+        the per-sequence lengths on the device. The list loops they replace
+        cost ~5 ms of host time per 16k tokens, during which the GPU had
+        nothing queued."""
+        lens = [len(s) for s in seqs]
+        cu = [0, *itertools.accumulate(lens)]
+        total = cu[-1]
+        ids = torch.from_numpy(np.fromiter(itertools.chain.from_iterable(s.token_ids for s in seqs),
+                                           dtype=np.int64, count=total))
+        lens_t = self._to_gpu(lens, torch.int64)
+        starts = self._to_gpu(cu[:-1], torch.int64)
+        pos = torch.arange(total, device=lens_t.device) - torch.repeat_interleave(starts, lens_t, output_size=total)
+        meta = dict(cu_seqlens_q=torch.tensor(cu), max_seqlen_q=max(lens))
+        if self.device == "cuda":
+            slots = self._to_gpu([s.slot for s in seqs], torch.int64)
+            blocks = _hip.prefill_blocks([(cu[i], n) for i, n in enumerate(lens)])
+            meta.update(slot_mapping=slots, attn_blocks=blocks.pin_memory().cuda(non_blocking=True),
+                        token_slots=torch.repeat_interleave(slots, lens_t, output_size=total))
+            ids = ids.pin_memory().cuda(non_blocking=True)
+        else:
+            meta.update(slot_mapping=torch.tensor([s.slot for s in seqs]))
+        with step_context(True, **meta):
+            hidden = self.model(ids, pos)
+        return hidden[self._to_gpu(cu[1:], torch.int64) - 1]

@@ -63,20 +63,30 @@ class LinearBase(nn.Module):
             self.quant_method = W8A8QuantMethod()
         else:
             self.quant_method = None
+        # Bumped by every weight_loader call: loaders write through
+        # `param.data`, which does not advance the parameter's _version, so
+        # caches derived from the weights key on this counter as well.
+        self.weights_generation = 0
         if self.quant_method is None:
             self.weight = nn.Parameter(torch.empty(output_size, input_size))
-            self.weight.weight_loader = self.weight_loader
+            self.weight.weight_loader = self._tracked(self.weight_loader)
         else:
             self.quant_method.create_weights(self, input_size, output_size)
-            self.qweight.weight_loader = self.qweight_loader
+            self.qweight.weight_loader = self._tracked(self.qweight_loader)
             for name in ("scales", "w_scales"):
                 if hasattr(self, name):
-                    getattr(self, name).weight_loader = self.scales_loader
+                    getattr(self, name).weight_loader = self._tracked(self.scales_loader)
         if bias:
             self.bias = nn.Parameter(torch.empty(output_size))
-            self.bias.weight_loader = self.bias_loader
+            self.bias.weight_loader = self._tracked(self.bias_loader)
         else:
             self.register_parameter("bias", None)
+
+    def _tracked(self, loader):
+        def load(*args, **kwargs):
+            loader(*args, **kwargs)
+            self.weights_generation += 1
+        return load
 
     def weight_loader(self, param: nn.Parameter, loaded_weight: torch.Tensor):
         param.data.copy_(loaded_weight)

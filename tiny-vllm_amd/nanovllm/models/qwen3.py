@@ -202,22 +202,39 @@ class Qwen3MLP(nn.Module):
     # gate_up output never reaches HBM; the result is bit-identical).
     GLU_MIN_TOKENS = 4096
 
+    def glu_shape_ok(self) -> bool:
+        """The fused gate_up kernel needs K % 128 == 0 (K <= 2^22) and the
+        intermediate size a multiple of 32 (its 32-row gate/up blocks); other
+        shapes take the unfused path."""
+        n2, k = self.gate_up_proj.qweight.shape
+        return k % 128 == 0 and k <= (1 << 22) and n2 % 64 == 0
+
     def forward(self, x) -> torch.Tensor:
         if (self.fuse_quant and isinstance(x, QuantizedActivation) and x.is_cuda and
-                x.xq.shape[0] >= self.GLU_MIN_TOKENS and _get_w8a8_backend_preference() == "native"):
+                x.xq.shape[0] >= self.GLU_MIN_TOKENS and _get_w8a8_backend_preference() == "native"
+                and self.glu_shape_ok()):
             return self.down_proj(self._glu_quant(x))
         return self.down_proj(self.act_fn(self.gate_up_proj(x), quant=self.fuse_quant))
+
+    def _glu_key(self) -> tuple:
+        """Identity of gate_up's current weights: the parameter objects
+        themselves (re-assignment), their storage and in-place versions, and
+        the layer's loader counter (loaders write through .data, which does
+        not advance _version)."""
+        lin = self.gate_up_proj
+        return (id(lin.qweight), id(lin.w_scales), lin.qweight.data_ptr(), lin.w_scales.data_ptr(),
+                lin.qweight._version, lin.w_scales._version, lin.weights_generation)
 
     def _glu_quant(self, x: "QuantizedActivation") -> "QuantizedActivation":
         lin = self.gate_up_proj
         # gate/up rows regrouped once per weight state (an extra copy of
         # gate_up's weights; the decode path keeps the original layout). The
-        # key follows in-place updates (copy_ bumps _version) and re-allocation;
-        # load_weights also drops the copy.
-        key = (lin.qweight.data_ptr(), lin.qweight._version, lin.w_scales.data_ptr(), lin.w_scales._version)
+        # cache holds the parameters it was built from, so their ids cannot
+        # be reused by new tensors while it is alive; load_weights also drops it.
+        key = self._glu_key()
         cache = getattr(self, "_glu_weights", None)
-        if cache is None or cache[0] != key:
-            cache = (key, *_hip.glu_interleave(lin.qweight.data, lin.w_scales.data))
+        if cache is None or cache[0] != key or cache[3] is not lin.qweight or cache[4] is not lin.w_scales:
+            cache = (key, *_hip.glu_interleave(lin.qweight.data, lin.w_scales.data), lin.qweight, lin.w_scales)
             self._glu_weights = cache
         h = _hip.w8a8_gemm_glu(x.xq, x.scales, cache[1], cache[2], out_dtype=x.dtype)
         q, s = _hip.act_quant(h)

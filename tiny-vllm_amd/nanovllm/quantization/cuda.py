@@ -9,13 +9,16 @@ line format (cuda.py:36-109). "cuda" is torch's device namespace, which on
 ROCm means the HIP device; the native backend is the gfx950 HIP library
 behind the C ABI (`_hip.py`).
 
-Behavioural difference from the reference, on purpose: the reference catches
-any native-kernel exception and silently recomputes with the torch path
-(cuda.py:345-356, 487-503). Here a failure of the native path on GPU tensors
-raises, so a broken or missing HIP library can never hide behind a slower
-path. The torch path runs only when asked for (`*_BACKEND=fallback`) or for
-tensors that are not on a GPU at all, and both are logged as
-`path=python_fallback` exactly like the reference.
+Failure handling follows the reference (cuda.py:344-356, 487-503): when the
+native call raises (an unsupported shape or alignment, a launch error), the
+failure is logged once as `path=python_fallback reason=native_unavailable ...`
+and the torch path computes the result. Two deliberate differences:
+* `NANOVLLM_NATIVE_STRICT=1` turns that fallback off, so the exception
+  propagates. Tests, the smoke check and the benchmark set it, so no
+  measurement or parity check can be served by the torch path.
+* A missing or unloadable HIP library always raises (it is a broken install,
+  not a per-call condition), so a GPU deployment can never run on the slower
+  torch path without noticing.
 """
 from __future__ import annotations
 
@@ -51,6 +54,11 @@ def _get_backend_preference() -> str:
 def _get_w8a8_backend_preference() -> str:
     value = os.environ.get("NANOVLLM_W8A8_BACKEND", "native").strip().lower()
     return value if value in _SUPPORTED_W8A8_BACKENDS else "native"
+
+
+def _strict_native() -> bool:
+    """NANOVLLM_NATIVE_STRICT: re-raise native failures instead of falling back."""
+    return os.environ.get("NANOVLLM_NATIVE_STRICT", "").strip().lower() not in _OFF_VALUES
 
 
 def _get_phase() -> str:
@@ -150,8 +158,15 @@ def apply_int8_weight_only_linear(x: torch.Tensor, qweight: torch.Tensor, scales
     if backend in ("cutlass", "auto"):
         _log_backend_event_once(backend="cutlass", phase=_get_phase(), path="unavailable", x=x, qweight=qweight,
                                 reason="no CUTLASS on ROCm; served by the native HIP kernels")
-    return native_int8_weight_only_linear(x, qweight, scales, bias)
-
+    _hip.load_library()  # a missing library is never hidden behind the torch path
+    try:
+        return native_int8_weight_only_linear(x, qweight, scales, bias)
+    except Exception as exc:
+        if _strict_native():
+            raise
+        _log_backend_event_once(backend="fallback", phase=_get_phase(), path="python_fallback", x=x,
+                                qweight=qweight, reason=f"native_unavailable {type(exc).__name__}: {exc}")
+        return int8_weight_only_linear_fallback(x, qweight, scales, bias)
 
 def _validate_w8a8(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,
                    bias: torch.Tensor | None, out_dtype: torch.dtype) -> None:
@@ -208,7 +223,16 @@ def apply_w8a8_linear(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.
                                      qweight=qweight, out_dtype=out_dtype, reason=reason)
         y = w8a8_linear_fallback(x_q, a_scales, qweight, w_scales, bias, out_dtype)
     else:
-        y = native_w8a8_linear(x_q, a_scales, qweight, w_scales, bias, out_dtype)
+        _hip.load_library()  # a missing library is never hidden behind the torch path
+        try:
+            y = native_w8a8_linear(x_q, a_scales, qweight, w_scales, bias, out_dtype)
+        except Exception as exc:
+            if _strict_native():
+                raise
+            _log_w8a8_backend_event_once(backend="fallback", phase=_get_phase(), path="python_fallback", x_q=x_q,
+                                         qweight=qweight, out_dtype=out_dtype,
+                                         reason=f"native_unavailable {type(exc).__name__}: {exc}")
+            y = w8a8_linear_fallback(x_q, a_scales, qweight, w_scales, bias, out_dtype)
     return y if out_shape is None else y.view(out_shape)
 
 

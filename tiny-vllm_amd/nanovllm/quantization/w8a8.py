@@ -6,7 +6,8 @@ from torch import nn
 from nanovllm.quantization import _hip
 from nanovllm.quantization.activation import QuantizedActivation
 from nanovllm.quantization.base import QuantMethod
-from nanovllm.quantization.cuda import _get_w8a8_backend_preference, apply_w8a8_linear, native_w8a8_fused_linear
+from nanovllm.quantization.cuda import (_get_phase, _get_w8a8_backend_preference, _log_w8a8_backend_event_once,
+                                       _strict_native, apply_w8a8_linear, native_w8a8_fused_linear)
 from nanovllm.quantization.utils import quantize_int8_per_row_dynamic
 
 
@@ -40,7 +41,19 @@ class W8A8QuantMethod(QuantMethod):
         if _native(x, layer.qweight, layer.w_scales, bias):
             # quantize + GEMM in one ABI call (reference w8a8.py:25-40 does
             # quantize_activation then apply_w8a8_linear; same numerics).
-            return native_w8a8_fused_linear(x, layer.qweight, layer.w_scales, bias)
+            _hip.load_library()  # a missing library is never hidden behind the torch path
+            try:
+                return native_w8a8_fused_linear(x, layer.qweight, layer.w_scales, bias)
+            except Exception as exc:
+                if _strict_native():
+                    raise
+                # the reference's fallback (cuda.py:487-503): log once, then torch
+                _log_w8a8_backend_event_once(backend="fallback", phase=_get_phase(), path="python_fallback",
+                                             x_q=x, qweight=layer.qweight, out_dtype=x.dtype,
+                                             reason=f"native_unavailable {type(exc).__name__}: {exc}")
+                x_q, a_scales = quantize_int8_per_row_dynamic(x.contiguous().view(-1, x.shape[-1]))
+                return apply_w8a8_linear(x_q, a_scales, layer.qweight, layer.w_scales, bias=bias,
+                                         out_dtype=x.dtype, out_shape=(*x.shape[:-1], layer.qweight.shape[0]))
         x_q, a_scales = self.quantize_activation(x)
         return apply_w8a8_linear(x_q, a_scales, layer.qweight, layer.w_scales, bias=bias, out_dtype=x.dtype,
                                  out_shape=(*x.shape[:-1], layer.qweight.shape[0]))

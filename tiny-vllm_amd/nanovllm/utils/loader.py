@@ -1,77 +1,99 @@
-"""safetensors -> model parameters, with the quantized-artifact checks
-(reference: nanovllm/utils/loader.py).
+"""Checkpoint and quantized-artifact loading into the model's parameters.
 
-Every tensor is routed to its parameter's `weight_loader` hook (which does the
-TP sharding); names of unpacked checkpoints (q_proj, k_proj, gate_proj, ...)
-are mapped onto the packed parameters through the model's
-`packed_modules_mapping`. After loading an "int8" or "w8a8" model, every
-`*.qweight` and `*.scales` / `*.w_scales` parameter must have been loaded,
-otherwise RuntimeError lists the missing ones (reference loader.py:27-41).
+What it must do (the artifact contract of nanovllm/utils/loader.py:27-68 and
+scripts/quantize.py): every tensor of every `*.safetensors` file in the
+directory goes to the `weight_loader` hook of its parameter, which does the
+tensor-parallel sharding. Unpacked checkpoint names (q_proj, k_proj, v_proj,
+gate_proj, up_proj) land in the packed parameter named by the model's
+`packed_modules_mapping`, with the shard id as the loader's extra argument.
+After an "int8" / "w8a8" load every `*.qweight` and `*.scales` /
+`*.w_scales` parameter must have been written, otherwise a RuntimeError
+names the missing ones (same message as the reference, since tooling may
+match on it).
+
+How: the name -> (parameter, loader args) resolution is computed once per
+model into a table (`_ParamIndex`), tensors are streamed file by file, and
+the bookkeeping of what was written is a set of parameter names checked at
+the end against the quantization mode's required suffixes.
 """
 from __future__ import annotations
 
 import os
+from dataclasses import dataclass
 from glob import glob
 
 import torch
 from safetensors import safe_open
 from torch import nn
 
+# quantization mode -> (label used in the error, required scale suffix)
+_REQUIRED = {"int8": ("INT8", "scales"), "w8a8": ("W8A8", "w_scales")}
+
 
 def default_weight_loader(param: nn.Parameter, loaded_weight: torch.Tensor):
+    """Loader of parameters without a hook: plain copy."""
     param.data.copy_(loaded_weight)
 
 
-def _has_parameter(model: nn.Module, name: str) -> bool:
-    try:
-        model.get_parameter(name)
-    except AttributeError:
-        return False
-    return True
+@dataclass(frozen=True)
+class _Target:
+    name: str
+    param: nn.Parameter
+    args: tuple
 
 
-def _load(model: nn.Module, name: str, tensor: torch.Tensor, loaded: set[str], *args) -> None:
-    param = model.get_parameter(name)
-    getattr(param, "weight_loader", default_weight_loader)(param, tensor, *args)
-    loaded.add(name)
+class _ParamIndex:
+    """Resolves checkpoint tensor names to model parameters."""
+
+    def __init__(self, model: nn.Module):
+        self.params = dict(model.named_parameters())
+        # longest source keys first, so e.g. "up_proj" never shadows a longer
+        # key that contains it
+        mapping = getattr(model, "packed_modules_mapping", {})
+        self.packed = sorted(mapping.items(), key=lambda kv: -len(kv[0]))
+
+    def resolve(self, tensor_name: str) -> _Target:
+        if tensor_name in self.params:
+            return _Target(tensor_name, self.params[tensor_name], ())
+        for src, (dst, shard_id) in self.packed:
+            if src in tensor_name:
+                name = tensor_name.replace(src, dst)
+                return _Target(name, self._param(name, tensor_name), (shard_id,))
+        return _Target(tensor_name, self._param(tensor_name, tensor_name), ())
+
+    def _param(self, name: str, tensor_name: str) -> nn.Parameter:
+        try:
+            return self.params[name]
+        except KeyError:
+            raise AttributeError(f"checkpoint tensor {tensor_name!r} has no parameter {name!r} in the model") from None
+
+    def required(self, scale_suffix: str) -> set[str]:
+        return {n for n in self.params if n.endswith(".qweight") or n.endswith("." + scale_suffix)}
 
 
-def _validate_quantized_loaded(model: nn.Module, loaded: set[str], scale_suffix: str, label: str) -> None:
-    expected = {n for n, _ in model.named_parameters() if n.endswith(".qweight") or n.endswith(scale_suffix)}
-    missing = sorted(expected - loaded)
-    if missing:
-        preview = ", ".join(missing[:8])
-        if len(missing) > 8:
-            preview += f", ... ({len(missing)} missing total)"
-        raise RuntimeError(f"Missing {label} quantized tensors. Expected qweight/{scale_suffix[1:]} for quantized "
-                           f"linear layers, but did not load: {preview}")
+def _missing_error(label: str, scale_suffix: str, missing: list[str]) -> RuntimeError:
+    shown = ", ".join(missing[:8])
+    if len(missing) > 8:
+        shown += f", ... ({len(missing)} missing total)"
+    return RuntimeError(f"Missing {label} quantized tensors. Expected qweight/{scale_suffix} for quantized "
+                        f"linear layers, but did not load: {shown}")
 
 
 def load_model(model: nn.Module, path: str, quantization: str | None = None) -> None:
-    mapping = getattr(model, "packed_modules_mapping", {})
-    loaded: set[str] = set()
-    files = glob(os.path.join(path, "*.safetensors"))
+    files = sorted(glob(os.path.join(path, "*.safetensors")))
     if not files:
         raise FileNotFoundError(f"No safetensors files found in {path}")
+    index = _ParamIndex(model)
+    written: set[str] = set()
     for file in files:
         with safe_open(file, "pt", "cpu") as f:
-            for name in f.keys():
-                tensor = f.get_tensor(name)
-                if _has_parameter(model, name):
-                    _load(model, name, tensor, loaded)
-                    continue
-                for key, (packed, shard_id) in mapping.items():
-                    if key in name:
-                        _load(model, name.replace(key, packed), tensor, loaded, shard_id)
-                        break
-                else:
-                    _load(model, name, tensor, loaded)
-    if quantization == "int8":
-        _validate_quantized_loaded(model, loaded, ".scales", "INT8")
-    elif quantization == "w8a8":
-        _validate_quantized_loaded(model, loaded, ".w_scales", "W8A8")
-    # derived weight copies (the MLP's regrouped gate_up for the fused
-    # SiLU-and-mul GEMM) are rebuilt from the new weights on next use
-    for mod in model.modules():
-        if hasattr(mod, "_glu_weights"):
-            del mod._glu_weights
+            for tensor_name in f.keys():
+                target = index.resolve(tensor_name)
+                loader = getattr(target.param, "weight_loader", default_weight_loader)
+                loader(target.param, f.get_tensor(tensor_name), *target.args)
+                written.add(target.name)
+    if quantization in _REQUIRED:
+        label, suffix = _REQUIRED[quantization]
+        missing = sorted(index.required(suffix) - written)
+        if missing:
+            raise _missing_error(label, suffix, missing)
