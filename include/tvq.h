@@ -131,6 +131,24 @@ int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight,
                     float* a_scales_buf, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* Limits of tvq_w8a8_linear_noalloc's scratch array (per device). */
+#define TVQ_NOALLOC_MAX_XQ_BYTES (8ll << 20) /* M*K int8 activation codes */
+#define TVQ_NOALLOC_MAX_ROWS 65536ll         /* M (per-token scales) */
+
+/* tvq_w8a8_linear without caller scratch buffers: the activation codes, the
+ * per-token scales and the split-K workspace live in a static device array
+ * of the library (about 24.3 MiB per device, held until the process ends), so
+ * the call allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP-graph capture, tight serving
+ * loops, harnesses that forbid allocation). Same arguments and result as
+ * tvq_w8a8_linear without xq_buf / a_scales_buf / workspace. Rejects
+ * M > TVQ_NOALLOC_MAX_ROWS or M*K > TVQ_NOALLOC_MAX_XQ_BYTES with
+ * TVQ_E_UNSUPPORTED. Calls on one device share the array: calls that overlap
+ * on one GPU (other streams, unordered threads) race. */
+int tvq_w8a8_linear_noalloc(const void* x, int dtype, const int8_t* qweight,
+                            const float* w_scales, const void* bias, void* y,
+                            int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Size in bytes of a GEMM workspace that enables every split-K launch (see
  * the top of this file). No reference counterpart: the reference's kernels
  * never split K. */

@@ -332,3 +332,15 @@ def test_missing_library_is_never_hidden(monkeypatch):
     lay, x, q, s = _cpu_layer(Int8WeightOnlyQuantMethod(), 32, 64)
     with pytest.raises(RuntimeError, match="not found"):
         cuda.apply_int8_weight_only_linear(x, q, s)
+
+
+def test_noalloc_linear_rejects_sizes_beyond_its_scratch(hiplib):
+    """The size limits are checked before any device work (no GPU needed)."""
+    big_k = 1024
+    m = (8 << 20) // big_k + 1  # one row past TVQ_NOALLOC_MAX_XQ_BYTES
+    rc = hiplib.tvq_w8a8_linear_noalloc(None, 1, None, None, None, None, m, 64, big_k, None)
+    assert rc == -2
+    assert b"scratch maximum" in hiplib.tvq_last_error()
+    rc = hiplib.tvq_w8a8_linear_noalloc(None, 1, None, None, None, None, 65537, 64, 16, None)
+    assert rc == -2
+    assert hiplib.tvq_w8a8_linear_noalloc(None, 1, None, None, None, None, -1, 64, 16, None) == -1

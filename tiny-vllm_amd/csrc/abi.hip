@@ -79,6 +79,8 @@ int run_gemm(const GemmArgs& a, void* stream) {
 
 }  // namespace
 
+int report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
   if (!aligned) return Path::kGeneric;

@@ -50,6 +50,9 @@ hipError_t launch_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_sc
 hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
                             hipStream_t stream);
 
+// Records `msg` as this thread's tvq_last_error() and returns `code`.
+int report_error(int code, const char* msg);
+
 // Path selection (pure function of shape and pointer alignment).
 Path select_gemm_path(const GemmArgs& a);
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned);

@@ -42,6 +42,7 @@ SYMBOLS = (
     ("tvq_w8a8_gemm_i32", _INT, (_VP, _VP, _VP, _I64, _I64, _I64, _VP, _I64, _VP)),
     ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _I64, _VP)),
     ("tvq_gemm_workspace_bytes", _I64, ()),
+    ("tvq_w8a8_linear_noalloc", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP)),
     ("tvq_rmsnorm", _INT, (_VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_silu_mul", _INT, (_VP, _VP, _VP, _VP, _INT, _I64, _I64, _VP)),
     ("tvq_w8a8_gemm_glu", _INT, (_VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP)),
