@@ -9,15 +9,24 @@ Infinity Cache, so weights come from HBM). Steps are captured in a HIP graph
 and replayed (the C ABI never allocates or syncs), so the timed region is GPU
 work, not Python launch overhead.
 
+Cache discipline: before the timed replay, a 1 GiB device copy (read and
+write, outside the timed region) evicts the 256 MB Infinity Cache and the L2s,
+and the timed steps use weight copies the warm-up never touched, so every
+timed step reads its weights from HBM at any --steps.
+
 Extra keys on the same line:
   roofline      the dominant kernel (the W8A8 GEMM) timed with HIP events on
                 its launch stream: algorithmic bytes / average launch time
   cpu_baseline  the reference's torch path (quantize -> dequantize -> F.linear)
                 restated in CPU torch, timed on this host's cores
-  sweep         configs 1-4: every (mode, shape, M) kernel with time, GB/s,
-                TOPS and roofline fraction (--quick skips it)
+  targets       the three north-star targets, from the sweep and the E2E leg
+  e2e           config 5: random-init Qwen3-0.6B through LLM.generate, bf16 vs
+                W8A16 vs W8A8 prefill / decode tok/s and TTFT (run first, in a
+                child process, before this process touches the GPU)
+  sweep         configs 1-4, one compact entry per (mode, shape, M):
+                "cfg mode MxNxK path us frac" (full records: gpurun_out/bench_sweep.jsonl)
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--no-e2e]
 """
 from __future__ import annotations
 
@@ -25,6 +34,7 @@ import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -210,7 +220,12 @@ def run_sweep(lib, dev, quick=False):
     cases = sweep_cases()
     if quick:
         cases = [c for c in cases if c[0] in ("cfg1", "cfg2") or (c[0].startswith("cfg3") and c[1] == "w8a8")]
-    for tag, mode, m, n, k in cases:
+    # full records go to a file (the JSON line carries a compact form)
+    (ROOT / "gpurun_out").mkdir(exist_ok=True)
+    log = open(ROOT / "gpurun_out" / "bench_sweep.jsonl", "w")
+    for ci, (tag, mode, m, n, k) in enumerate(cases):
+        if ci % 16 == 0:
+            print(f"sweep case {ci}/{len(cases)}", file=sys.stderr, flush=True)
         x, qs, ss = make_inputs(mode, m, n, k, dev)
         copies = len(qs)
         if mode == "w8a8":
@@ -233,9 +248,11 @@ def run_sweep(lib, dev, quick=False):
             rec["act_quant_us"] = round(tq * 1e6, 3)
             rec["act_quant_gbs"] = round(act_quant_bytes(m, k) / tq / 1e9, 1)
         out.append(rec)
-        print(json.dumps(rec), file=sys.stderr, flush=True)
+        log.write(json.dumps(rec) + "\n")
+        log.flush()
         del x, qs, ss, y
         torch.cuda.empty_cache()
+    log.close()
     return out
 
 
@@ -304,6 +321,66 @@ def run_profile_case(spec):
                           weight_copies=len(qs))), flush=True)
 
 
+# ---------------------------------------------------------------- config 5 (end to end)
+
+def run_e2e(timeout_s=420):
+    """Config 5 through the engine (nanovllm.bench_e2e) in a child process:
+    256 sequences, inputs and outputs uniform 100-1024, greedy, bf16 vs W8A16
+    vs W8A8 on a random-init Qwen3-0.6B. Started before this process
+    initialises the GPU; its report comes back through a JSON file."""
+    out = ROOT / "gpurun_out" / "bench_e2e.json"
+    out.parent.mkdir(exist_ok=True)
+    if out.exists():
+        out.unlink()
+    cmd = [sys.executable, "-m", "nanovllm.bench_e2e", "--modes", "bf16,int8,w8a8", "--output", str(out)]
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([str(ROOT / "tiny-vllm_amd"), os.environ.get("PYTHONPATH", "")]))
+    t0 = time.perf_counter()
+    proc = subprocess.run(cmd, env=env, stdout=sys.stderr, stderr=sys.stderr, timeout=timeout_s)
+    if proc.returncode != 0 or not out.is_file():
+        raise RuntimeError(f"e2e leg failed with exit code {proc.returncode}")
+    rep = json.loads(out.read_text())
+    res = {}
+    for r in rep["results"]:
+        res[r["mode"]] = dict(prefill_tok_s=round(r["prefill_tokens_per_second"]),
+                              decode_tok_s=round(r["decode_tokens_per_second"]),
+                              total_tok_s=round(r["throughput_tokens_per_second"]),
+                              ttft_s=round(r["ttft_seconds_approx"] or 0.0, 4), wall_s=round(r["wall_time_seconds"], 2),
+                              tokens=r["total_tokens"])
+    base = res.get("bf16")
+    if base:
+        for mode, r in res.items():
+            if mode != "bf16":
+                r["prefill_vs_bf16"] = round(r["prefill_tok_s"] / base["prefill_tok_s"], 3)
+                r["decode_vs_bf16"] = round(r["decode_tok_s"] / base["decode_tok_s"], 3)
+    res["workload"] = ("random-init Qwen3-0.6B (28 layers), 256 seqs, input/output lengths uniform 100-1024, "
+                       "greedy, max_num_batched_tokens 16384, HIP-graph decode")
+    res["leg_seconds"] = round(time.perf_counter() - t0, 1)
+    return res
+
+
+def targets_from(sweep, e2e):
+    """The north-star targets: W8A16 decode >= 0.70 of HBM at M <= 64, W8A8
+    prefill >= 0.50 of int8 peak at M = 8192, E2E W8A8 prefill > bf16."""
+    t = {}
+    if sweep:
+        dec = [r for r in sweep if r["mode"] == "w8a16" and r["M"] <= 64]
+        if dec:
+            t["w8a16_decode_hbm_frac_m_le_64"] = dict(min=min(r["frac"] for r in dec), max=max(r["frac"] for r in dec),
+                                                      target=0.70)
+        pre = [r for r in sweep if r["mode"] == "w8a8" and r["M"] == 8192]
+        if pre:
+            t["w8a8_prefill_i8_frac_m8192"] = dict(min=min(r["frac"] for r in pre), max=max(r["frac"] for r in pre),
+                                                   target=0.50)
+    if e2e and "w8a8" in e2e and "prefill_vs_bf16" in e2e["w8a8"]:
+        t["e2e_w8a8_prefill_vs_bf16"] = dict(value=e2e["w8a8"]["prefill_vs_bf16"], target=">1")
+    return t
+
+
+def compact(sweep):
+    return [f'{r["cfg"]} {r["mode"]} {r["M"]}x{r["N"]}x{r["K"]} {r["path"]} {r["us"]}us {r["frac"]}'
+            + (f' aq{r["act_quant_us"]}us' if "act_quant_us" in r else "") for r in sweep]
+
+
 # ---------------------------------------------------------------- main
 
 def main():
@@ -314,6 +391,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="only configs 1-2 and W8A8 prefill in the sweep")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 engine leg")
     ap.add_argument("--profile", action="store_true",
                     help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
@@ -325,12 +403,14 @@ def main():
         run_profile_case(args.profile_case)
         return
     if args.profile:
-        args.no_sweep = args.no_cpu = True
+        args.no_sweep = args.no_cpu = args.no_e2e = True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the quantized linear is a per-GPU kernel; sharding is a design note). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    e2e = None if args.no_e2e else run_e2e()
 
     from nanovllm.quantization import _hip
     lib = _hip.load_library()
@@ -354,10 +434,17 @@ def main():
     a_s = torch.empty(m, dtype=torch.float32, device=dev)
 
     # Headline: exactly `steps` W8A8 linears, graph-replayed, weights rotating.
-    g_warm = _graph([L.w8a8_linear(x, qs[i % copies], ss[i % copies], y, xq, a_s) for i in range(args.warmup)])
+    # Warm-up steps use the copies at the end of the pool, timed steps start at
+    # copy 0, and a 1 GiB copy between them evicts every cache level.
+    g_warm = _graph([L.w8a8_linear(x, qs[copies - 1 - i % copies], ss[copies - 1 - i % copies], y, xq, a_s)
+                     for i in range(args.warmup)])
     g_step = _graph([L.w8a8_linear(x, qs[i % copies], ss[i % copies], y, xq, a_s) for i in range(args.steps)])
+    flush_src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    flush_dst = torch.empty_like(flush_src)
     g_warm.replay()
+    flush_dst.copy_(flush_src)
     torch.cuda.synchronize()
+    del flush_src, flush_dst
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -410,7 +497,9 @@ def main():
         },
         "roofline": roof,
         "cpu_baseline": cpu,
-        "sweep": sweep,
+        "targets": targets_from(sweep, e2e),
+        "e2e": e2e,
+        "sweep": None if sweep is None else compact(sweep),
     }
     print(json.dumps(line), flush=True)
 
