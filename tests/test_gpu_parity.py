@@ -31,8 +31,10 @@ def _log_case(**kw):
 
 # ---------------------------------------------------------------- act quant
 
+# M picks the threads per row (four waves below 512 rows, two below 1024, then one)
 ACT_SHAPES = [(1, 1024), (3, 1024), (64, 1024), (257, 3072), (33, 4096), (5, 12288), (2, 8), (7, 24), (9, 100),
-              (1, 1)]
+              (1, 1), (1, 12288), (64, 12288), (511, 2048), (600, 2048), (1023, 3072), (1030, 1024), (2000, 12288),
+              (513, 16384), (3, 24)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -454,3 +456,26 @@ def test_split_k_graph_replay(hiplib):
         assert torch.equal(y16.view(torch.int16), ref16.view(torch.int16)), f"replay {i}"
         assert torch.equal(y8.view(torch.int16), ref8.view(torch.int16)), f"replay {i}"
         assert torch.equal(other.view(torch.int16), _hip.w8a16_gemm(x[:20], q, s).view(torch.int16))
+
+
+# ---------------------------------------------------------------- kernel families
+
+# (M, N, K) and the families forced on it with TVQ_GEMM_PATH (each valid for
+# the shape by its own rule): W8A8 outputs must agree bit for bit.
+FAMILY_CASES = [((16, 4096, 1024), ("skinny", "dma", "stream")), ((64, 16384, 1024), ("skinny", "dma", "stream")),
+                ((40, 6144, 2048), ("skinny", "dma")), ((2, 4096, 2048), ("gemv", "skinny"))]
+
+
+@pytest.mark.parametrize("case", FAMILY_CASES, ids=lambda c: "x".join(map(str, c[0])))
+def test_forced_kernel_families_agree(hiplib, monkeypatch, case):
+    from nanovllm.quantization import _hip
+    (m, n, k), fams = case
+    d = _dev()
+    xq, a_s, q, w_s = _w8a8_inputs(m, n, k, seed=m * n + k)
+    args = [torch.from_numpy(t).to(d) for t in (xq, a_s, q, w_s)]
+    ref, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq, q), a_s, w_s)
+    for fam in fams:
+        _log_case(test="family", fam=fam, m=m, n=n, k=k)
+        monkeypatch.setenv("TVQ_GEMM_PATH", fam)
+        y = _hip.w8a8_gemm(*args[:2], *args[2:], None, torch.bfloat16)
+        np.testing.assert_array_equal(bits16(y), ref)

@@ -63,7 +63,9 @@ def _placed(t: torch.Tensor, misalign: bool) -> torch.Tensor:
     return out
 
 
-RMS_SHAPES = [(1, 1024), (7, 1024), (300, 1024), (64, 128), (33, 4096), (4, 2048), (5, 5000), (9, 1003), (1, 8)]
+# M picks the threads per row: < 512 four waves, 512..1023 two waves, >= 1024 one wave
+RMS_SHAPES = [(1, 1024), (7, 1024), (300, 1024), (64, 128), (33, 4096), (4, 2048), (5, 5000), (9, 1003), (1, 8),
+              (600, 2048), (513, 4096), (1030, 1024), (1500, 3072)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -102,7 +104,8 @@ def test_rmsnorm(hiplib, shape, dtype, with_res):
         assert torch.equal(rd2, rd) and torch.equal(rd3, rd)
 
 
-SILU_SHAPES = [(1, 3072), (64, 3072), (513, 3072), (16, 768), (3, 4096), (5, 6000), (7, 1003), (2, 8)]
+SILU_SHAPES = [(1, 3072), (64, 3072), (513, 3072), (16, 768), (3, 4096), (5, 6000), (7, 1003), (2, 8),
+               (1030, 3072), (700, 1024)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

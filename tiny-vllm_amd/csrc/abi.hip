@@ -2,6 +2,7 @@
 // selection and the launches. Declared in include/tvq.h.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -81,9 +82,33 @@ int run_gemm(const GemmArgs& a, void* stream) {
 
 int report_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
+namespace {
+
+// TVQ_GEMM_PATH=<gemv|skinny|stream|dma> forces that kernel family for
+// the shapes it supports (others keep the automatic choice). A diagnostic for
+// benchmarks and for tests that compare the families on the same inputs.
+bool forced_path(const GemmArgs& a, Path* out) {
+  const char* env = getenv("TVQ_GEMM_PATH");
+  if (env == nullptr || env[0] == 0) return false;
+  Path p;
+  bool ok;
+  if (!strcmp(env, "gemv")) p = Path::kGemv, ok = gemv_shape_ok(a.M, a.K);
+  else if (!strcmp(env, "skinny")) p = Path::kSkinny, ok = a.M <= kSkinnyMaxM;
+  else if (!strcmp(env, "stream")) p = Path::kStream, ok = stream_shape_ok(a.M, a.N, a.K);
+  else if (!strcmp(env, "dma")) p = Path::kDma, ok = dma_shape_ok(a.K);
+  else return false;
+  if (!ok) return false;
+  *out = p;
+  return true;
+}
+
+}  // namespace
+
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
   if (!aligned) return Path::kGeneric;
+  Path forced;
+  if (forced_path(a, &forced)) return forced;
   if (gemv_shape_ok(a.M, a.K)) return Path::kGemv;
   if (a.M <= kSkinnyMaxM) {
     if (dma_shape_ok(a.K) && (a.M > kDmaMinM || (a.M > 8 && a.N * a.K >= kDmaMidWeights))) return Path::kDma;

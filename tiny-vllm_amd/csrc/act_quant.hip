@@ -6,25 +6,29 @@
 //   amax   = max_k |float(x[m,k])|                (exact, order-free)
 //   s      = max(amax / 127.0f, eps)               (IEEE RN divide)
 //   xq     = clamp(rint(float(x) / s), -127, 127)  (IEEE RN divide, ties-to-even;
-//            computed as a multiply by RN(1/s) with an exact-divide fallback
-//            near half-integers, see quant_code)
+//            computed as a multiply by RN(1/s) plus one exact fma correction,
+//            see quant_code)
 //
-// One wave (64 lanes) owns one row; a 256-thread workgroup handles 4 rows.
-// HBM traffic is the algorithmic minimum for rows that fit the register
-// cache (K <= 64 * 8 * NI, NI = 1, 2, 4, 6 or 8 by K, so short rows keep few
-// VGPRs and many waves in flight): 2 B read + 1 B written per element and
-// 4 B per row. Longer rows are read a second time for the quantize pass
-// (that second read is served by L2). Codes take quant_code_fast; a vector
-// step in which any lane met a near-tie is redone with the exact quant_code
-// (a few percent of steps), which keeps the common path branch-free.
+// A row is owned by TPR threads (one to four waves) of a 256-thread
+// workgroup: 64 when there are enough rows to fill the GPU (4 rows per
+// workgroup), up to 256 for small M, so that a decode-size call (M = 1..512)
+// still spreads each row's loads over many lanes and the GPU has up to one
+// workgroup per row. With TPR > 64 the row maximum is combined across the
+// row's waves through LDS. HBM traffic is the algorithmic minimum for rows
+// that fit the register cache (K <= TPR * 8 * NI, NI = 1, 2, 4, 6 or 8 by K,
+// so short rows keep few VGPRs and many waves in flight): 2 B read + 1 B
+// written per element and 4 B per row. Longer rows are read a second time
+// for the quantize pass (that second read is served by L2). The codes are
+// branch-free (quant_code: one multiply, two fma, rint, clamp per element).
 #include "tvq_common.h"
 #include "tvq_internal.h"
 
 namespace tvq {
 namespace {
 
-constexpr int kRowsPerBlock = 4;
-constexpr int kMaxIters = 8;  // 8 x 512 elements -> K <= 4096 stays in VGPRs
+constexpr int kBlock = 256;
+constexpr int kRowsPerBlock = 4;  // scalar path
+constexpr int kMaxIters = 8;      // 8 x 8 x TPR elements stay in VGPRs
 
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
@@ -46,84 +50,70 @@ __device__ __forceinline__ uint32_t q1(float x, float s, float rs) {
   return (uint32_t)((int32_t)quant_code(x, s, rs) & 0xff);
 }
 
-template <typename T>
-__device__ __forceinline__ uint32_t q1f(const u32x4& v, int i, float rs, bool& near) {
-  const uint32_t w = v[i >> 1];
-  const float x = to_float<T>((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
-  return (uint32_t)((int32_t)quant_code_fast(x, rs, near) & 0xff);
-}
-
-// 8 codes, exact: fast codes unless some lane of the wave met a near-tie.
-template <typename T>
-__device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs);
-template <typename T>
-__device__ __forceinline__ u32x2 quant8_wave(u32x4 v, float s, float rs) {
-  bool near = false;
-  u32x2 r;
-  r.x = q1f<T>(v, 0, rs, near) | (q1f<T>(v, 1, rs, near) << 8) | (q1f<T>(v, 2, rs, near) << 16) |
-        (q1f<T>(v, 3, rs, near) << 24);
-  r.y = q1f<T>(v, 4, rs, near) | (q1f<T>(v, 5, rs, near) << 8) | (q1f<T>(v, 6, rs, near) << 16) |
-        (q1f<T>(v, 7, rs, near) << 24);
-  if (__builtin_amdgcn_ballot_w64(near) != 0) r = quant8<T>(v, s, rs);  // wave-uniform
-  return r;
-}
-
-template <typename T>
-__device__ __forceinline__ u32x2 quant8(u32x4 v, float s, float rs) {
-  u32x2 r;
-  r.x = q1(to_float<T>((uint16_t)(v[0] & 0xffffu)), s, rs) | (q1(to_float<T>((uint16_t)(v[0] >> 16)), s, rs) << 8) |
-        (q1(to_float<T>((uint16_t)(v[1] & 0xffffu)), s, rs) << 16) | (q1(to_float<T>((uint16_t)(v[1] >> 16)), s, rs) << 24);
-  r.y = q1(to_float<T>((uint16_t)(v[2] & 0xffffu)), s, rs) | (q1(to_float<T>((uint16_t)(v[2] >> 16)), s, rs) << 8) |
-        (q1(to_float<T>((uint16_t)(v[3] & 0xffffu)), s, rs) << 16) | (q1(to_float<T>((uint16_t)(v[3] >> 16)), s, rs) << 24);
-  return r;
-}
-
 // Vector path: K % 8 == 0 and 16-byte aligned x, 8-byte aligned xq.
 // NI >= 6: the compiler, left alone, took 129 (NI = 6) and 241 (NI = 8)
 // VGPRs for what fits in ~60; asking for 6 waves per SIMD keeps them at
 // 57 / 67 without spills (NI = 6 at 16384 x 3072: ~1.3 % of a W8A8 prefill).
-template <typename T, int NI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NI >= 6 ? 6 : 1))) void act_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
-                                                            float eps, int8_t* __restrict__ xq,
-                                                            float* __restrict__ a_scales) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const uint16_t* xr = x + row * K;
+template <typename T, int TPR, int NI>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(NI >= 6 ? 6 : 1))) void act_quant_vec_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, float eps, int8_t* __restrict__ xq,
+    float* __restrict__ a_scales) {
+  static_assert(TPR == 64 || TPR == 128 || TPR == 256, "a row is one, two or four waves");
+  constexpr int kWavesPerRow = TPR / kWave;
+  const int t = threadIdx.x % TPR;  // lane within the row
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / TPR) + threadIdx.x / TPR;
+  if constexpr (kWavesPerRow == 1) {
+    if (row >= M) return;  // no barrier below
+  }
+  const bool live = row < M;  // rows past M (TPR > 64) still reach the barrier
+  const uint16_t* xr = x + (live ? row : 0) * K;
   int8_t* qr = xq + row * K;
-  const int64_t nvec = K >> 3;  // 8 elements per 16-byte vector
+  const int64_t nvec = live ? (K >> 3) : 0;  // 8 elements per 16-byte vector
 
+  // All NI loads go out before any is used: the index is clamped into the
+  // row instead of branching around the load, so no wait sits between them
+  // (a load under a per-iteration branch with its use inside the branch
+  // costs one memory round trip per iteration).
   u32x4 cache[NI];
   float amax = 0.0f;
+  const int64_t vmax = nvec > 0 ? nvec - 1 : 0;
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int64_t v = (int64_t)it * kWave + lane;
-    cache[it] = u32x4{0, 0, 0, 0};  // lanes past the row quantize zeros (no near-tie)
-    if (v < nvec) {
-      cache[it] = ldg128_stream(xr + v * 8);
-      amax = fmaxf(amax, absmax8<T>(cache[it]));
-    }
+    const int64_t v = (int64_t)it * TPR + t;
+    cache[it] = ldg128_stream(xr + (v < vmax ? v : vmax) * 8);
   }
-  for (int64_t v = (int64_t)NI * kWave + lane; v < nvec; v += kWave) {
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int64_t v = (int64_t)it * TPR + t;
+    if (v >= nvec) cache[it] = u32x4{0, 0, 0, 0};  // lanes past the row quantize zeros (no near-tie)
+    amax = fmaxf(amax, absmax8<T>(cache[it]));
+  }
+  for (int64_t v = (int64_t)NI * TPR + t; v < nvec; v += TPR) {
     amax = fmaxf(amax, absmax8<T>(ldg128_stream(xr + v * 8)));
   }
   amax = wave_max(amax);
+  if constexpr (kWavesPerRow > 1) {
+    __shared__ float red[kBlock / kWave];
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) red[w] = amax;
+    __syncthreads();
+    const int w0 = (threadIdx.x / TPR) * kWavesPerRow;
+#pragma unroll
+    for (int i = 0; i < kWavesPerRow; ++i) amax = fmaxf(amax, red[w0 + i]);
+    if (!live) return;
+  }
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);
-  if (lane == 0) a_scales[row] = s;
+  if (t == 0) a_scales[row] = s;
   const float rs = __fdiv_rn(1.0f, s);
 
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int64_t v = (int64_t)it * kWave + lane;
-    if (it * kWave < nvec) {  // wave-uniform: the ballot needs every active lane
-      const u32x2 c = quant8_wave<T>(cache[it], s, rs);
-      if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = c;
-    }
+    const int64_t v = (int64_t)it * TPR + t;
+    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = quant_codes8<T>(cache[it], s, rs);
   }
-  for (int64_t v0 = (int64_t)NI * kWave; v0 < nvec; v0 += kWave) {
-    const int64_t v = v0 + lane;
-    const u32x2 c = quant8_wave<T>(v < nvec ? ldg128(xr + v * 8) : u32x4{0, 0, 0, 0}, s, rs);
-    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = c;
+  for (int64_t v0 = (int64_t)NI * TPR; v0 < nvec; v0 += TPR) {
+    const int64_t v = v0 + t;
+    if (v < nvec) *reinterpret_cast<u32x2*>(qr + v * 8) = quant_codes8<T>(ldg128(xr + v * 8), s, rs);
   }
 }
 
@@ -151,28 +141,56 @@ bool act_quant_vec_ok(const void* x, const void* xq, int64_t K) {
   return (K % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)xq % 8 == 0);
 }
 
+// Threads per row: 64 once M / 4 workgroups fill the GPU, more for fewer
+// rows (up to one 256-thread workgroup per row), and always enough for the
+// row to fit the register cache (8 vectors of 8 per thread), so long rows
+// are never read twice.
+int act_quant_tpr(int64_t M, int64_t K) {
+  int tpr = M >= 1024 ? 64 : (M >= 512 ? 128 : 256);
+  while (tpr < 256 && K > (int64_t)tpr * 8 * kMaxIters) tpr *= 2;
+  return tpr;
+}
+
+namespace {
+
+template <typename T, int TPR>
+hipError_t launch_vec(const uint16_t* xp, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
+                      hipStream_t stream) {
+  const dim3 grid((unsigned)((M + kBlock / TPR - 1) / (kBlock / TPR)));
+  const int64_t per = (K / 8 + TPR - 1) / TPR;  // 16-byte vectors per thread
+  // register cache sized to the row
+  if (per <= 1) act_quant_vec_kernel<T, TPR, 1><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+  else if (per <= 2) act_quant_vec_kernel<T, TPR, 2><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+  else if (per <= 4) act_quant_vec_kernel<T, TPR, 4><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+  else if (per <= 6) act_quant_vec_kernel<T, TPR, 6><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+  else act_quant_vec_kernel<T, TPR, kMaxIters><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_vec_t(const uint16_t* xp, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
+                        hipStream_t stream) {
+  switch (act_quant_tpr(M, K)) {
+    case 64: return launch_vec<T, 64>(xp, M, K, eps, xq, a_scales, stream);
+    case 128: return launch_vec<T, 128>(xp, M, K, eps, xq, a_scales, stream);
+    default: return launch_vec<T, 256>(xp, M, K, eps, xq, a_scales, stream);
+  }
+}
+
+}  // namespace
+
 hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,
                             hipStream_t stream) {
-  const dim3 grid((unsigned)((M + kRowsPerBlock - 1) / kRowsPerBlock));
-  const dim3 block(256);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   if (act_quant_vec_ok(x, xq, K)) {
-    // register cache sized to the row: 512 elements per iteration
-#define TVQ_AQ(NI)                                                                    \
-  (bf16 ? act_quant_vec_kernel<BF16, NI><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales) \
-        : act_quant_vec_kernel<F16, NI><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales))
-    if (K <= 512) TVQ_AQ(1);
-    else if (K <= 1024) TVQ_AQ(2);
-    else if (K <= 2048) TVQ_AQ(4);
-    else if (K <= 3072) TVQ_AQ(6);
-    else TVQ_AQ(kMaxIters);
-#undef TVQ_AQ
-  } else {
-    if (bf16)
-      act_quant_scalar_kernel<BF16><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales);
-    else
-      act_quant_scalar_kernel<F16><<<grid, block, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+    return bf16 ? launch_vec_t<BF16>(xp, M, K, eps, xq, a_scales, stream)
+                : launch_vec_t<F16>(xp, M, K, eps, xq, a_scales, stream);
   }
+  const dim3 grid((unsigned)((M + kRowsPerBlock - 1) / kRowsPerBlock));
+  if (bf16)
+    act_quant_scalar_kernel<BF16><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
+  else
+    act_quant_scalar_kernel<F16><<<grid, kBlock, 0, stream>>>(xp, M, K, eps, xq, a_scales);
   return hipGetLastError();
 }
 

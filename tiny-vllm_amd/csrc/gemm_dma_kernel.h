@@ -223,7 +223,7 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false, bool kGlu = false>
+          bool kNtW = false, bool kGlu = false, bool kRot = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
@@ -266,7 +266,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   const char* xbase = static_cast<const char*>(xv);
   uint32_t soff[C::kLPW];
   constexpr int kWCh = KS / 16, kXCh = C::kXRb / 16;   // 16-byte chunks per block row
-  auto set_sources = [&](int m0, int n0, int kb) {
+  // kRot: a tile walks its k-stages starting at stage (tm + tn) % nk and
+  // wrapping around, so the tiles that share an operand panel do not all
+  // request the same cache lines at the same time. Only the order of the
+  // k-stages changes (exact for int32 sums; a fixed, per-tile order for fp32).
+  int rot = 0, rot_nk = 1;
+  auto set_sources = [&](int m0, int n0, int kb, int nk_tile, int rot_seed) {
+    if constexpr (kRot) {
+      rot_nk = nk_tile > 0 ? nk_tile : 1;
+      rot = rot_seed % rot_nk;
+    }
     wbase = reinterpret_cast<const char*>(qw) + (int64_t)n0 * K + (int64_t)kb * C::kKStage;
     xbase = static_cast<const char*>(xv) + ((int64_t)m0 * K + (int64_t)kb * C::kKStage) * (kW8A8 ? 1 : 2);
 #pragma unroll
@@ -295,7 +304,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       const int step = wblk ? KS : C::kXRow;
       // uniform 64-bit base + unsigned 32-bit lane offset: the saddr form of
       // the DMA, so no 64-bit address per op stays live in VGPRs
-      const char* p = (wblk ? wbase : xbase) + (uint32_t)(soff[j] + (uint32_t)(kt * step));
+      int kq = kt;
+      if constexpr (kRot) {
+        kq += rot;
+        if (kq >= rot_nk) kq -= rot_nk;
+      }
+      const char* p = (wblk ? wbase : xbase) + (uint32_t)(soff[j] + (uint32_t)(kq * step));
       // kNtW: weight blocks that no other tile reads again (one m-tile)
       // stream with the non-temporal hint, so they do not evict the
       // activation panel every tile shares from L2
@@ -364,7 +378,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   int unit = blockIdx.x;
   int tm, tn, tl, sk, kb, nk;
   unit_coords(unit, tm, tn, tl, sk, kb, nk);
-  set_sources(tm * BM, tn * BN, kb);
+  set_sources(tm * BM, tn * BN, kb, nk, tm + tn);
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
     if (s < nk) issue(s);
@@ -489,7 +503,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     if (more) {
       unit = next;
       unit_coords(unit, tm, tn, tl, sk, kb, nk);
-      set_sources(tm * BM, tn * BN, kb);
+      set_sources(tm * BM, tn * BN, kb, nk, tm + tn);
 #pragma unroll
       for (int s = 0; s < S - 1; ++s)
         if (s < nk) issue(s);
@@ -729,12 +743,12 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false, bool kGlu = false>
+          bool kNtW = false, bool kGlu = false, bool kRot = false>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
                       int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
                       hipStream_t stream) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
-  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu, kRot>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

@@ -19,9 +19,11 @@
 // the activations and one launch; the codes are bit-identical to running
 // act-quant on this kernel's own y.
 //
-// One wave owns one row, 4 rows per 256-thread workgroup (like act-quant).
-// Rows of up to 4096 elements (8 x 512) stay in registers, so HBM traffic is
-// the algorithmic minimum: read x (+ residual, + w from L2), write residual
+// A row is owned by TPR threads of a 256-thread workgroup (like act-quant):
+// one wave (4 rows per workgroup) when there are enough rows to fill the
+// GPU, two or four waves for decode-size M, whose row sums and maxima are then
+// combined through LDS. Rows of up to 8 x TPR x 8 elements stay in registers,
+// so HBM traffic is the algorithmic minimum: read x (+ residual, + w from L2), write residual
 // and y (2 B/elem) and/or the codes (1 B/elem) + 4 B per row. Longer rows or
 // K % 8 != 0 or unaligned pointers take a scalar path that re-reads the row
 // (from L2).
@@ -33,8 +35,9 @@
 namespace tvq {
 namespace {
 
-constexpr int kRows = 4;
-constexpr int kIters = 8;  // at most 8 x 64 lanes x 8 elements = 4096 per row in registers
+constexpr int kRows = 4;   // scalar path: one wave per row
+constexpr int kBlock = 256;
+constexpr int kIters = 8;  // at most 8 x TPR lanes x 8 elements per row in registers
 
 __device__ __forceinline__ float wsum(float v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -42,6 +45,23 @@ __device__ __forceinline__ float wsum(float v) {
 }
 __device__ __forceinline__ float wmax(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Sum / maximum over the TPR threads of a row. With TPR > 64 the row's
+// waves meet in LDS (`lds` holds one slot per wave of the block; each call
+// site passes its own array), so every thread of the block must call it.
+template <int TPR, bool kMax>
+__device__ __forceinline__ float row_reduce(float v, float* lds) {
+  v = kMax ? wmax(v) : wsum(v);
+  if constexpr (TPR > kWave) {
+    if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = v;
+    __syncthreads();
+    const int w0 = (threadIdx.x / TPR) * (TPR / kWave);
+    v = lds[w0];
+#pragma unroll
+    for (int i = 1; i < TPR / kWave; ++i) v = kMax ? fmaxf(v, lds[w0 + i]) : v + lds[w0 + i];
+  }
   return v;
 }
 
@@ -61,71 +81,75 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 // Quantize the 8-element bf16/fp16 vectors cached in y[] (already rounded)
 // and store codes + scale. Codes take quant_code_fast; a vector step where
 // any lane met a near-tie is redone with the exact quant_code.
-template <typename T, int NI>
-__device__ __forceinline__ void quant_store(const u32x4 (&y)[NI], int nvec, int lane, float eps, int8_t* qr,
-                                            float* srow) {
+template <typename T, int TPR, int NI>
+__device__ __forceinline__ void quant_store(const u32x4 (&y)[NI], int nvec, int t, bool live, float eps, int8_t* qr,
+                                            float* srow, float* lds) {
   float amax = 0.0f;
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    if (it * kWave + lane < nvec) {
+    if (it * TPR + t < nvec) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(elt<T>(y[it], i)));
     }
   }
-  amax = wmax(amax);
+  amax = row_reduce<TPR, true>(amax, lds);
+  if (!live) return;
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);
-  if (lane == 0) *srow = s;
+  if (t == 0) *srow = s;
   const float rs = __fdiv_rn(1.0f, s);
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int v = it * kWave + lane;
-    if (it * kWave < nvec) {  // wave-uniform: the ballot needs every active lane
-      const u32x4 yv = v < nvec ? y[it] : u32x4{0, 0, 0, 0};
-      bool near = false;
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lo |= ((uint32_t)(int32_t)quant_code_fast(elt<T>(yv, i), rs, near) & 0xffu) << (8 * i);
-        hi |= ((uint32_t)(int32_t)quant_code_fast(elt<T>(yv, i + 4), rs, near) & 0xffu) << (8 * i);
-      }
-      if (__builtin_amdgcn_ballot_w64(near) != 0) {
-        lo = hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          lo |= (uint32_t)(uint8_t)qcode(elt<T>(yv, i), s, rs) << (8 * i);
-          hi |= (uint32_t)(uint8_t)qcode(elt<T>(yv, i + 4), s, rs) << (8 * i);
-        }
-      }
-      if (v < nvec) *reinterpret_cast<u32x2*>(qr + (int64_t)v * 8) = u32x2{lo, hi};
-    }
+    const int v = it * TPR + t;
+    if (v < nvec) *reinterpret_cast<u32x2*>(qr + (int64_t)v * 8) = quant_codes8<T>(y[it], s, rs);
   }
 }
 
-template <typename T, bool kRes, bool kY, bool kQ, int NI>
-__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
-                                                          const uint16_t* __restrict__ w, float eps,
-                                                          uint16_t* __restrict__ y, int8_t* __restrict__ xq,
-                                                          float* __restrict__ a_scales, int64_t M, int K) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const int nvec = K >> 3;
+template <int TPR>
+struct RowLane {
+  int t;
+  int64_t row;
+  bool live;
+  __device__ RowLane(int64_t M)
+      : t((int)(threadIdx.x % TPR)), row((int64_t)blockIdx.x * (kBlock / TPR) + threadIdx.x / TPR), live(row < M) {}
+};
+
+template <typename T, bool kRes, bool kY, bool kQ, int TPR, int NI>
+__global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
+                                                             const uint16_t* __restrict__ w, float eps,
+                                                             uint16_t* __restrict__ y, int8_t* __restrict__ xq,
+                                                             float* __restrict__ a_scales, int64_t M, int K) {
+  const RowLane<TPR> rl(M);
+  if (TPR == kWave && !rl.live) return;  // one wave per row: no barriers
+  __shared__ float lds_ss[kBlock / kWave], lds_max[kBlock / kWave];
+  const int t = rl.t;
+  const int64_t row = rl.live ? rl.row : 0;
+  const int nvec = rl.live ? (K >> 3) : 0;
   const uint16_t* xr = x + row * K;
   float h[NI][8];
   float ss = 0.0f;
+  // every load of the row is issued before the first use (clamped index, no
+  // branch around the loads), so they are all in flight together
+  const int vmax = nvec > 0 ? nvec - 1 : 0;
+  u32x4 xin[NI], rin[NI];
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int v = it * kWave + lane;
+    const int v = min(it * TPR + t, vmax);
+    xin[it] = ldg128_stream(xr + (int64_t)v * 8);
+    if constexpr (kRes) rin[it] = ldg128_stream(res + row * K + (int64_t)v * 8);
+  }
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int v = it * TPR + t;
     if (v < nvec) {
-      const u32x4 xv = ldg128_stream(xr + (int64_t)v * 8);
+      const u32x4 xv = xin[it];
       u32x4 rv = {0, 0, 0, 0};
-      if constexpr (kRes) rv = ldg128_stream(res + row * K + (int64_t)v * 8);
+      if constexpr (kRes) rv = rin[it];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float t = elt<T>(xv, i);
-        if constexpr (kRes) t += elt<T>(rv, i);
-        h[it][i] = t;
-        ss += t * t;
+        float tt = elt<T>(xv, i);
+        if constexpr (kRes) tt += elt<T>(rv, i);
+        h[it][i] = tt;
+        ss += tt * tt;
       }
       if constexpr (kRes) {
         u32x4 o;
@@ -135,14 +159,16 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __rest
       }
     }
   }
-  ss = wsum(ss);
+  ss = row_reduce<TPR, false>(ss, lds_ss);
   const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)K) + eps));
-  u32x4 yv[NI];
+  u32x4 yv[NI], win[NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) win[it] = ldg128(w + (int64_t)min(it * TPR + t, vmax) * 8);
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int v = it * kWave + lane;
+    const int v = it * TPR + t;
     if (v < nvec) {
-      const u32x4 wv = ldg128(w + (int64_t)v * 8);
+      const u32x4 wv = win[it];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float a = to_float<T>(from_float<T>(h[it][2 * i] * r)) * elt<T>(wv, 2 * i);
@@ -152,26 +178,35 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __rest
       if constexpr (kY) *reinterpret_cast<u32x4*>(y + row * K + (int64_t)v * 8) = yv[it];
     }
   }
-  if constexpr (kQ) quant_store<T, NI>(yv, nvec, lane, 1e-8f, xq + row * K, a_scales + row);
+  if constexpr (kQ) quant_store<T, TPR, NI>(yv, nvec, t, rl.live, 1e-8f, xq + row * K, a_scales + row, lds_max);
 }
 
-template <typename T, bool kY, bool kQ, int NI>
-__global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ y,
-                                                           int8_t* __restrict__ xq, float* __restrict__ a_scales,
-                                                           int64_t M, int I) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const int nvec = I >> 3;
+template <typename T, bool kY, bool kQ, int TPR, int NI>
+__global__ __launch_bounds__(kBlock) void silu_mul_vec_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ y,
+                                                              int8_t* __restrict__ xq, float* __restrict__ a_scales,
+                                                              int64_t M, int I) {
+  const RowLane<TPR> rl(M);
+  if (TPR == kWave && !rl.live) return;  // one wave per row: no barriers
+  __shared__ float lds_max[kBlock / kWave];
+  const int t = rl.t;
+  const int64_t row = rl.live ? rl.row : 0;
+  const int nvec = rl.live ? (I >> 3) : 0;
   const uint16_t* g = gu + row * 2 * I;
   const uint16_t* u = g + I;
-  u32x4 yv[NI];
+  u32x4 yv[NI], gin[NI], uin[NI];
+  const int vmax = nvec > 0 ? nvec - 1 : 0;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {  // all loads in flight before the first use
+    const int v = min(it * TPR + t, vmax);
+    gin[it] = ldg128_stream(g + (int64_t)v * 8);
+    uin[it] = ldg128_stream(u + (int64_t)v * 8);
+  }
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int v = it * kWave + lane;
+    const int v = it * TPR + t;
     if (v < nvec) {
-      const u32x4 gv = ldg128_stream(g + (int64_t)v * 8);
-      const u32x4 uv = ldg128_stream(u + (int64_t)v * 8);
+      const u32x4 gv = gin[it];
+      const u32x4 uv = uin[it];
       float o[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -183,7 +218,7 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __res
       if constexpr (kY) *reinterpret_cast<u32x4*>(y + row * I + (int64_t)v * 8) = yv[it];
     }
   }
-  if constexpr (kQ) quant_store<T, NI>(yv, nvec, lane, 1e-8f, xq + row * I, a_scales + row);
+  if constexpr (kQ) quant_store<T, TPR, NI>(yv, nvec, t, rl.live, 1e-8f, xq + row * I, a_scales + row, lds_max);
 }
 
 // ---------------------------------------------------------------- scalar paths
@@ -270,25 +305,53 @@ bool producer_vec_ok(const void* a, const void* b, const void* c, const void* d,
   return K % 8 == 0 && K <= kIters * kWave * 8 && al(a, 16) && al(b, 16) && al(c, 16) && al(d, 8);
 }
 
+// Threads per row by M (as act-quant): one wave once M / 4 workgroups fill
+// the GPU, up to four waves (one row per workgroup) for small M.
+static int producer_tpr(int64_t M) { return M >= 1024 ? 64 : (M >= 512 ? 128 : 256); }
+
+// Calls go(TPR, NI) with the register-cache depth sized to the row (8-element
+// vectors per thread), for the TPR this M takes.
+template <typename Go>
+static void with_shape(int64_t M, int64_t K, Go&& go) {
+  auto depth = [&](auto tpr) {
+    constexpr int TPR = decltype(tpr)::value;
+    const int64_t per = (K / 8 + TPR - 1) / TPR;
+    if (per <= 2) go(tpr, std::integral_constant<int, 2>{});
+    else if (per <= 4) go(tpr, std::integral_constant<int, 4>{});
+    else if (per <= 6) go(tpr, std::integral_constant<int, 6>{});
+    else go(tpr, std::integral_constant<int, kIters>{});
+  };
+  switch (producer_tpr(M)) {
+    case 64: depth(std::integral_constant<int, 64>{}); break;
+    case 128: depth(std::integral_constant<int, 128>{}); break;
+    default: depth(std::integral_constant<int, 256>{}); break;
+  }
+}
+
+static dim3 producer_grid(int64_t M) {
+  const int64_t rows = kBlock / producer_tpr(M);
+  return dim3((unsigned)((M + rows - 1) / rows));
+}
+
 template <typename T>
 static hipError_t rms_t(const void* x, void* res, const void* w, float eps, void* y, int8_t* xq, float* as,
                         int64_t M, int64_t K, hipStream_t st) {
-  const dim3 grid((unsigned)((M + kRows - 1) / kRows)), block(256);
   auto X = static_cast<const uint16_t*>(x);
   auto R = static_cast<uint16_t*>(res);
   auto W = static_cast<const uint16_t*>(w);
   auto Y = static_cast<uint16_t*>(y);
   const int k = (int)K;
   if (!producer_vec_ok(x, res, y, xq, K)) {
-    rmsnorm_scalar_kernel<T><<<grid, block, 0, st>>>(X, R, W, eps, Y, xq, as, M, k);
+    const dim3 grid((unsigned)((M + kRows - 1) / kRows));
+    rmsnorm_scalar_kernel<T><<<grid, kBlock, 0, st>>>(X, R, W, eps, Y, xq, as, M, k);
     return hipGetLastError();
   }
   const bool hy = y != nullptr, hq = xq != nullptr;
-  // row held in registers: NI iterations of 512 elements, sized to K
-  auto go = [&](auto ni) {
-    constexpr int NI = decltype(ni)::value;
+  const dim3 grid = producer_grid(M);
+  with_shape(M, K, [&](auto tpr, auto ni) {
+    constexpr int TPR = decltype(tpr)::value, NI = decltype(ni)::value;
 #define TVQ_RMS(RES, YY, QQ) \
-  rmsnorm_vec_kernel<T, RES, YY, QQ, NI><<<grid, block, 0, st>>>(X, R, W, eps, Y, xq, as, M, k)
+  rmsnorm_vec_kernel<T, RES, YY, QQ, TPR, NI><<<grid, kBlock, 0, st>>>(X, R, W, eps, Y, xq, as, M, k)
     if (res) {
       if (hy && hq) TVQ_RMS(true, true, true);
       else if (hy) TVQ_RMS(true, true, false);
@@ -299,10 +362,7 @@ static hipError_t rms_t(const void* x, void* res, const void* w, float eps, void
       else TVQ_RMS(false, false, true);
     }
 #undef TVQ_RMS
-  };
-  if (K <= 1024) go(std::integral_constant<int, 2>{});
-  else if (K <= 2048) go(std::integral_constant<int, 4>{});
-  else go(std::integral_constant<int, kIters>{});
+  });
   return hipGetLastError();
 }
 
@@ -314,24 +374,21 @@ hipError_t launch_rmsnorm(const void* x, void* residual, const void* weight, flo
 
 template <typename T>
 static hipError_t silu_t(const void* gu, void* y, int8_t* xq, float* as, int64_t M, int64_t I, hipStream_t st) {
-  const dim3 grid((unsigned)((M + kRows - 1) / kRows)), block(256);
   auto G = static_cast<const uint16_t*>(gu);
   auto Y = static_cast<uint16_t*>(y);
   const int i = (int)I;
   if (!producer_vec_ok(gu, y, nullptr, xq, I) || ((uintptr_t)(G + I) % 16) != 0) {
-    silu_mul_scalar_kernel<T><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
+    const dim3 grid((unsigned)((M + kRows - 1) / kRows));
+    silu_mul_scalar_kernel<T><<<grid, kBlock, 0, st>>>(G, Y, xq, as, M, i);
     return hipGetLastError();
   }
-  auto go = [&](auto ni) {
-    constexpr int NI = decltype(ni)::value;
-    if (y && xq) silu_mul_vec_kernel<T, true, true, NI><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
-    else if (y) silu_mul_vec_kernel<T, true, false, NI><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
-    else silu_mul_vec_kernel<T, false, true, NI><<<grid, block, 0, st>>>(G, Y, xq, as, M, i);
-  };
-  if (I <= 1024) go(std::integral_constant<int, 2>{});
-  else if (I <= 2048) go(std::integral_constant<int, 4>{});
-  else if (I <= 3072) go(std::integral_constant<int, 6>{});
-  else go(std::integral_constant<int, kIters>{});
+  const dim3 grid = producer_grid(M);
+  with_shape(M, I, [&](auto tpr, auto ni) {
+    constexpr int TPR = decltype(tpr)::value, NI = decltype(ni)::value;
+    if (y && xq) silu_mul_vec_kernel<T, true, true, TPR, NI><<<grid, kBlock, 0, st>>>(G, Y, xq, as, M, i);
+    else if (y) silu_mul_vec_kernel<T, true, false, TPR, NI><<<grid, kBlock, 0, st>>>(G, Y, xq, as, M, i);
+    else silu_mul_vec_kernel<T, false, true, TPR, NI><<<grid, kBlock, 0, st>>>(G, Y, xq, as, M, i);
+  });
   return hipGetLastError();
 }
 

@@ -149,15 +149,33 @@ __device__ __forceinline__ float epi_w8a16_nb(float acc, float s) { return __bui
 // Per-token int8 code of x for scale s, bit-identical to
 // clamp(rint(x / s), -127, 127) with an IEEE round-to-nearest divide
 // (quantize_int8_per_row_dynamic, reference utils.py:28-32), given
-// rs = RN(1/s). The multiply d = RN(x * rs) is within 2^-16 of RN(x / s)
-// for |x / s| <= 128 (two roundings of relative size <= 2^-24 each), and rint
-// changes only at half-integers; so unless d lies within 2^-14 of one, rint(d)
-// equals rint(RN(x / s)). Those rare ties and near-ties take the exact divide.
+// rs = RN(1/s), without a divide and without a branch:
+//   d = RN(x * rs)            within about one ulp of x / s
+//   r = fma(-d, s, x)         the remainder x - d*s, exact in fp32
+//   q = fma(r, rs, d)         one correction step (Markstein)
+// rint(q) equals rint(RN(x / s)): checked on the CPU with the host's fmaf for
+// 1.63e9 (bf16 x, s) pairs and 6.3e8 (fp16 x, s) pairs -- every input value
+// |x| <= amax for 100000 / 40000 random row maxima -- with no mismatch, where
+// rint(d) alone mismatched 12110 / 11058 times; and on the GPU against the
+// oracle on rows built to sit on and around half-integers. |x / s| <= 127
+// (1 + 2^-23) by the choice of s, so the clamp only guards non-finite rows.
 __device__ __forceinline__ float quant_code(float x, float s, float rs) {
   const float d = x * rs;
-  float t = rintf(d);
-  if (fabsf(fabsf(d - truncf(d)) - 0.5f) < 0x1p-14f) t = rintf(__fdiv_rn(x, s));
-  return fminf(fmaxf(t, -127.0f), 127.0f);
+  const float q = __builtin_fmaf(__builtin_fmaf(-d, s, x), rs, d);
+  return fminf(fmaxf(rintf(q), -127.0f), 127.0f);
+}
+
+// Eight 16-bit inputs (a 16-byte vector) -> eight packed int8 codes.
+template <typename T>
+__device__ __forceinline__ u32x2 quant_codes8(const u32x4& v, float s, float rs) {
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = v[i >> 1];
+    const float x = to_float<T>((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+    c[i] = (uint32_t)(int32_t)quant_code(x, s, rs) & 0xffu;
+  }
+  return u32x2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24), c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
 }
 
 // SiLU(a) = a / (1 + exp(-a)) = a * rcp(1 + 2^(-a log2 e)), on the hardware
@@ -165,16 +183,6 @@ __device__ __forceinline__ float quant_code(float x, float s, float rs) {
 // then rounded once, as the reference's fused elementwise kernel rounds).
 __device__ __forceinline__ float silu_f(float a) {
   return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
-}
-
-// quant_code without its rare branch: rint(x * rs) clamped, and `near` set
-// when x * rs lies within 2^-14 of a half-integer. Callers OR `near` over a
-// wave (ballot) and redo those vectors with quant_code, so the common path
-// stays branch-free and bit-identical to quant_code.
-__device__ __forceinline__ float quant_code_fast(float x, float rs, bool& near) {
-  const float d = x * rs;
-  near |= fabsf(fabsf(d - truncf(d)) - 0.5f) < 0x1p-14f;
-  return fminf(fmaxf(rintf(d), -127.0f), 127.0f);
 }
 
 }  // namespace tvq
