@@ -178,6 +178,12 @@ class Launcher:
         return lambda: self._ck(self.lib.tvq_w8a16_gemm(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None,
                                                         y.data_ptr(), m, n, k, *self.ws, self.stream()))
 
+    def operand_floor(self, op, x, q):
+        m, k = x.shape
+        n = q.shape[0]
+        return lambda: self._ck(self.lib.tvq_gemm_operand_floor(op, x.data_ptr(), q.data_ptr(), m, n, k,
+                                                                self.stream()))
+
     def _ck(self, rc):
         if rc != 0:
             raise RuntimeError(self.lib.tvq_last_error().decode())
@@ -244,6 +250,12 @@ def run_sweep(lib, dev, quick=False):
         r = roofline_for(mode, m, n, k, t)
         rec = dict(cfg=tag, mode=mode, M=m, N=n, K=k, path=path, us=round(t * 1e6, 3), gbs=round(r["gbs"], 1),
                    tops=round(r["tops"], 2), bound=r["bound"], frac=round(r["frac"], 4), weight_copies=copies)
+        if path.startswith("dma"):
+            # operand-delivery floor of the same tiles (unsplit), same weight copies
+            op = _hip.OP_W8A8 if mode == "w8a8" else _hip.OP_W8A16
+            xa = xq if mode == "w8a8" else x
+            tf = time_kernel(lambda i: L.operand_floor(op, xa, qs[i]), copies)
+            rec["floor_us"] = round(tf * 1e6, 3)
         if tq is not None:
             rec["act_quant_us"] = round(tq * 1e6, 3)
             rec["act_quant_gbs"] = round(act_quant_bytes(m, k) / tq / 1e9, 1)
@@ -378,6 +390,7 @@ def targets_from(sweep, e2e):
 
 def compact(sweep):
     return [f'{r["cfg"]} {r["mode"]} {r["M"]}x{r["N"]}x{r["K"]} {r["path"]} {r["us"]}us {r["frac"]}'
+            + (f' floor{r["floor_us"]}us' if "floor_us" in r else "")
             + (f' aq{r["act_quant_us"]}us' if "act_quant_us" in r else "") for r in sweep]
 
 
@@ -466,10 +479,14 @@ def main():
         rec = json.loads(tfile.read_text())
         if rec.get("kernel") == _hip.select_path(_hip.OP_W8A8, m, n, k):  # only for the kernel it measured
             traffic = rec.get("hbm_bytes_per_launch")
+    # The same tiles' operand stream alone (no MFMA, no output): the floor that
+    # the GEMM's data movement sets, over the same rotating weight copies.
+    t_floor = time_kernel(lambda i: L.operand_floor(_hip.OP_W8A8, xq0, qs[i]), copies, min_launches=256)
     roof = dict(bound=r["bound"], achieved=round(r["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
                 frac=round(r["gbs"] / PEAK_HBM_GBS, 4), traffic=traffic,
                 kernel=_hip.select_path(_hip.OP_W8A8, m, n, k), kernel_us=round(t_gemm * 1e6, 3),
-                algorithmic_bytes=r["bytes"], tops=round(r["tops"], 3))
+                algorithmic_bytes=r["bytes"], tops=round(r["tops"], 3),
+                operand_floor_us=round(t_floor * 1e6, 3), floor_over_kernel=round(t_floor / t_gemm, 4))
     del x, qs, ss
     torch.cuda.empty_cache()
 

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define TVQ_ABI_VERSION 3
+#define TVQ_ABI_VERSION 4
 
 /* Activation / output element types. */
 enum tvq_dtype {
@@ -111,6 +111,29 @@ int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales,
                   const void* bias, void* y, int out_dtype, int64_t M,
                   int64_t N, int64_t K, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/* W8A16 with the reference kernel's rounding: every weight is first
+ * dequantized to wd[n,k] = T(T(qweight[n,k]) * T(scales[n])) in the
+ * activation type T (bf16 or fp16), then y = out(sum_k x[m,k] * wd[n,k] +
+ * bias[n]) with fp32 accumulation and no further scaling. Replaces the
+ * dequantization of int8_weight_only_gemm_wmma_kernel
+ * (int8_weight_only_gemm.cu:397-413, epilogue 507-516), which
+ * int8_weight_only_linear_fallback (nanovllm/quantization/cuda.py:293-300)
+ * also applies, for callers that need those roundings rather than the fp32
+ * per-output scale of tvq_w8a16_gemm. Never splits K. */
+int tvq_w8a16_gemm_rounded(const void* x, int dtype, const int8_t* qweight,
+                           const float* scales, const void* bias, void* y,
+                           int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Measurement only, no reference counterpart: runs the operand stream of the
+ * DMA GEMM tiles that tvq_w8a16_gemm (op TVQ_OP_W8A16, x 16-bit) or
+ * tvq_w8a8_gemm (TVQ_OP_W8A8, x int8) would launch for this shape -- the same
+ * grid, tile walk, global->LDS transfers, waits and barriers, with the
+ * fragment reads, MFMAs and output compiled out (unsplit). Its time is the
+ * operand-delivery floor of that tiling. Writes no output. Needs K % 128 == 0
+ * and 16-byte aligned operands (TVQ_E_UNSUPPORTED otherwise). */
+int tvq_gemm_operand_floor(int op, const void* x, const int8_t* qweight,
+                           int64_t M, int64_t N, int64_t K, void* stream);
 
 /* The raw exact int32 accumulator acc[m,n] = sum_k xq[m,k]·qweight[n,k] of
  * the W8A8 path, written to y_i32 [M, N], using the same kernel selection as

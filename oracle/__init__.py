@@ -20,6 +20,8 @@ Parity status per function (see tests/test_oracle.py):
   w8a16_torch_path         pinned against the exact fp64 product (bound)
   w8a8_torch_path          pinned against the exact fp64 product (bound)
   w8a16_f64 / w8a8_f64     pinned (brute force on tiny inputs, C vs numpy)
+  w8a16_rounded_weights    pinned (CPU torch running the reference's expression,
+                           bit for bit; power-of-two scales; zero codes)
 """
 from __future__ import annotations
 
@@ -110,6 +112,28 @@ def w8a8_epilogue_bf16(acc: np.ndarray, a_s: np.ndarray, w_s: np.ndarray) -> np.
 def w8a16_f64(x_f32: np.ndarray, q: np.ndarray, s: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
     """Exact-arithmetic W8A16 product (x @ q^T) * s + b in float64."""
     y = (x_f32.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)[None, :]
+    if bias is not None:
+        y = y + bias.astype(np.float64)[None, :]
+    return y
+
+
+def w8a16_rounded_weights(q: np.ndarray, s: np.ndarray, is_bf16: bool = True) -> np.ndarray:
+    """The reference kernel's dequantized weight T(T(q) * T(s)) as float32
+    values (int8_weight_only_gemm.cu:401-411; the torch path's
+    qweight.to(T) * scales.to(T)[:, None], cuda.py:293-300). T(q) is exact, and
+    the product of two T values is exact in fp64, so one rounding to T gives
+    the rounded multiply."""
+    if is_bf16:
+        sr = bf16_bits_to_f32(f32_to_bf16_bits(s.astype(np.float32)))
+        prod = (q.astype(np.float32) * sr[:, None]).astype(np.float32)
+        return bf16_bits_to_f32(f32_to_bf16_bits(prod))
+    sr = s.astype(np.float16).astype(np.float32)
+    return (q.astype(np.float32) * sr[:, None]).astype(np.float16).astype(np.float32)
+
+
+def w8a16_rounded_f64(x_f32: np.ndarray, wd_f32: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """Exact x @ wd^T + b in float64 for the rounded-dequant mode."""
+    y = x_f32.astype(np.float64) @ wd_f32.astype(np.float64).T
     if bias is not None:
         y = y + bias.astype(np.float64)[None, :]
     return y

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(hiplib):
 
 
 def test_abi_version_and_errors_without_gpu(hiplib):
-    assert hiplib.tvq_abi_version() == 3
+    assert hiplib.tvq_abi_version() == 4
     assert hiplib.tvq_gemm_workspace_bytes() >= 16 << 20
     assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None, 0, None) == -1
     assert b"dtype" in hiplib.tvq_last_error()

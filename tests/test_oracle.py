@@ -410,3 +410,44 @@ def test_gemm_i32_blas_exact():
         np.testing.assert_array_equal(got, oracle.c_gemm_i32(xq, w))
         np.testing.assert_array_equal(got, oracle.gemm_i32(xq, w))
         assert got[0, 0] == -127 * 127 * k and got[0, 1] == 127 * 127 * k
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rounded_weights_match_reference_expression(dtype):
+    """w8a16_rounded_weights == CPU torch running the reference's dequant
+    expression qweight.to(T) * scales.to(T)[:, None] (cuda.py:293-300), bit for
+    bit, over scales spanning several binades and every int8 code."""
+    rng = np.random.default_rng(11)
+    q = np.tile(np.arange(-127, 128, dtype=np.int8), (64, 1))
+    s = (rng.random(64) * 10.0 ** rng.integers(-5, 0, size=64)).astype(np.float32) + np.float32(1e-6)
+    got = oracle.w8a16_rounded_weights(q, s, is_bf16=dtype == torch.bfloat16)
+    ref = (torch.from_numpy(q).to(dtype) * torch.from_numpy(s).to(dtype)[:, None]).float().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_rounded_weights_closed_forms():
+    q = np.array([[-127, -1, 0, 1, 5, 127]], dtype=np.int8)
+    # power-of-two scale: every product is exact in both types
+    for bf in (True, False):
+        wd = oracle.w8a16_rounded_weights(q, np.array([2.0 ** -10], np.float32), is_bf16=bf)
+        assert np.array_equal(wd, q.astype(np.float32) * np.float32(2.0 ** -10))
+    # q = 1 gives the rounded scale itself; 3 * bf16(1/3) rounds once more
+    s = np.array([1.0 / 3.0], np.float32)
+    wd = oracle.w8a16_rounded_weights(np.array([[1, 3]], np.int8), s, is_bf16=True)
+    s_bf = np.float32(0.333984375)              # bf16(1/3) = 0x3EAB
+    assert wd[0, 0] == s_bf
+    assert wd[0, 1] == np.float32(1.0)          # 3 * 0.333984375 = 1.001953125 -> bf16 1.0
+    wd16 = oracle.w8a16_rounded_weights(np.array([[3]], np.int8), s, is_bf16=False)
+    assert wd16[0, 0] == np.float32(np.float16(3 * np.float32(np.float16(1.0 / 3.0))))
+
+
+def test_rounded_f64_brute_force_tiny():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 7)).astype(np.float32)
+    wd = rng.standard_normal((4, 7)).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    y = oracle.w8a16_rounded_f64(x, wd, b)
+    for m in range(3):
+        for n in range(4):
+            assert y[m, n] == pytest.approx(sum(float(x[m, k]) * float(wd[n, k]) for k in range(7)) + float(b[n]),
+                                            rel=1e-15, abs=1e-15)

@@ -200,6 +200,34 @@ int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales, const int8_t* qweight
   return run_gemm(a, stream);
 }
 
+int tvq_w8a16_gemm_rounded(const void* x, int dtype, const int8_t* qweight, const float* scales, const void* bias,
+                           void* y, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dims(M, N, K)) return rc;
+  if (M == 0) return ok();
+  if (!x || !qweight || !scales || !y) return fail(TVQ_E_INVALID, "null pointer argument");
+  GemmArgs a{x, nullptr, qweight, scales, bias, y, M, N, K, false, dtype == TVQ_DTYPE_BF16, false};
+  const bool aligned = aligned16(x) && aligned16(qweight) && aligned16(y);
+  hipError_t e = (aligned && dma_shape_ok(K)) ? launch_dma_dq(a, (hipStream_t)stream)
+                                              : launch_generic_dq(a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int tvq_gemm_operand_floor(int op, const void* x, const int8_t* qweight, int64_t M, int64_t N, int64_t K,
+                           void* stream) {
+  if (op != TVQ_OP_W8A16 && op != TVQ_OP_W8A8) return fail(TVQ_E_INVALID, "op must be TVQ_OP_W8A16 or TVQ_OP_W8A8");
+  if (int rc = check_dims(M, N, K)) return rc;
+  if (M == 0) return ok();
+  if (!x || !qweight) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (!dma_shape_ok(K) || !aligned16(x) || !aligned16(qweight))
+    return fail(TVQ_E_UNSUPPORTED, "operand floor: the DMA tiles need K %% 128 == 0 and 16-byte aligned operands");
+  GemmArgs a{x, nullptr, qweight, nullptr, nullptr, nullptr, M, N, K, op == TVQ_OP_W8A8, true, false};
+  hipError_t e = launch_dma_floor(a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32, int64_t M, int64_t N, int64_t K,
                       void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = check_dims(M, N, K)) return rc;

@@ -466,7 +466,6 @@ __global__ __launch_bounds__(2 * kBlkQ * G) __attribute__((amdgpu_waves_per_eu(2
   constexpr int kWph = kBlkQ / 32;                     // waves per head
   constexpr int kThreads = 64 * kWph * G;
   constexpr int kVec = kBlkK * kD / 8;                 // 16-byte vectors per K (or V) tile
-  constexpr int kPer = kVec / kThreads;                // per thread
   static_assert(kBlkQ % 32 == 0 && kVec % kThreads == 0, "tile vectors split evenly");
   // unpadded 256-byte rows, 16-byte chunks XOR-swizzled per row (K: chunk ^
   // row % 16, V: chunk ^ 2 (row % 8)) so the fragment and transposing reads

@@ -213,6 +213,58 @@ hipError_t launch_dma_glu(const GemmArgs& a, hipStream_t stream) {
       stream);
 }
 
+namespace {
+
+// The operand-delivery floor of configuration c: the kernel with kDmaOnly,
+// unsplit, with the weight-stream hint the real launch uses.
+template <DmaCfg c>
+hipError_t floor_of(const GemmArgs& a, hipStream_t s) {
+  constexpr CfgInfo i = info<c>();
+  if (i.w8a8 && a.M <= 64)
+    return launch_dma<BF16, i.w8a8, false, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false, true, false, false, true>(
+        a.x, nullptr, a.qweight, nullptr, nullptr, nullptr, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr,
+        0, s);
+  return launch_dma<BF16, i.w8a8, false, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false, false, false, false, true>(
+      a.x, nullptr, a.qweight, nullptr, nullptr, nullptr, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0,
+      s);
+}
+
+}  // namespace
+
+// W8A16 with the reference's rounded dequantization (kDq), unsplit.
+template <typename T, DmaCfg c>
+hipError_t dq_of(const GemmArgs& a, hipStream_t s) {
+  constexpr CfgInfo i = info<c>();
+  return launch_dma<T, false, false, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, false, false, false, false, false, true>(
+      a.x, nullptr, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K, 8, m_major(a), 1, nullptr, 0, s);
+}
+
+template <typename T>
+hipError_t dq_t(const GemmArgs& a, hipStream_t s) {
+  switch (choose(false, a.M, a.N, a.K)) {
+    case DmaCfg::kH_128x256: return dq_of<T, DmaCfg::kH_128x256>(a, s);
+    case DmaCfg::kH_64x128: return dq_of<T, DmaCfg::kH_64x128>(a, s);
+    case DmaCfg::kH_32x64: return dq_of<T, DmaCfg::kH_32x64>(a, s);
+    case DmaCfg::kH_64x128w8: return dq_of<T, DmaCfg::kH_64x128w8>(a, s);
+    default: return dq_of<T, DmaCfg::kH_64x64>(a, s);
+  }
+}
+
+hipError_t launch_dma_dq(const GemmArgs& a, hipStream_t stream) {
+  return a.bf16 ? dq_t<BF16>(a, stream) : dq_t<F16>(a, stream);
+}
+
+hipError_t launch_dma_floor(const GemmArgs& a, hipStream_t stream) {
+  switch (choose(a.w8a8, a.M, a.N, a.K)) {
+#define TVQ_CASE(C) \
+  case DmaCfg::C: return floor_of<DmaCfg::C>(a, stream);
+    TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
+    TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
+#undef TVQ_CASE
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream) {
   if (a.w8a8) {
     if (a.raw_i32) return run<BF16, true, true>(a, stream);

@@ -68,11 +68,26 @@
 // result does not depend on arrival order; int32 sums are exact) and runs the
 // normal epilogue, then returns the counter to zero. The counters must be
 // zero when a call starts and are zero again when it ends.
+//
+// kDq (W8A16 only): each weight is dequantized to T(T(q) * T(s[n])) before
+// the MFMA, as the reference's kernel does, and the epilogue adds only the
+// bias (the scale is already inside the sum).
+//
+// kDmaOnly (measurement): the same grid, tile walk, DMA ops, waits and
+// barriers with the fragment reads, MFMAs, scale/bias loads and epilogue
+// compiled out: it reads only xv and qw (a_scales, ws, bias and yv may be
+// null) and writes nothing to global memory. Its time is the operand-delivery
+// floor of the tiling, against which the full kernel is judged.
 #pragma once
 
 #include <type_traits>
 
 #include "tvq_common.h"
+
+// Timeline hooks for instrumented builds (no code in the library).
+#ifndef TVQ_TL_MARK
+#define TVQ_TL_MARK(ev)
+#endif
 
 namespace tvq {
 namespace dma {
@@ -223,7 +238,7 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false, bool kGlu = false, bool kRot = false>
+          bool kNtW = false, bool kGlu = false, bool kRot = false, bool kDmaOnly = false, bool kDq = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
@@ -375,6 +390,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     }
   };
 
+  TVQ_TL_MARK(0);
   int unit = blockIdx.x;
   int tm, tn, tl, sk, kb, nk;
   unit_coords(unit, tm, tn, tl, sk, kb, nk);
@@ -382,12 +398,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
     if (s < nk) issue(s);
-  if constexpr (!kRaw) load_scales(tm * BM, tn * BN);
+  if constexpr (!kRaw && !kDmaOnly) load_scales(tm * BM, tn * BN);
 
+  static_assert(!kDq || !kW8A8, "rounded dequantization is a W8A16 mode");
   while (true) {
     const int n0 = tn * BN;
     const int m0 = tm * BM;
     const int cur_tl = tl, cur_sk = sk, cur_nk = nk;
+    // kDq: the rounded scale of the channel each weight fragment row holds
+    float dqs[kDq ? C::FN : 1];
+    if constexpr (kDq) {
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i) dqs[i] = round_to<T>(ws[min(n0 + wn * C::TN + MF * i + (lane % MF), N - 1)]);
+    }
     Acc acc[C::FN][C::FM];
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
@@ -421,10 +444,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 
     wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 1));
     barrier();
+    TVQ_TL_MARK(1);
     // after the barrier: the previous tile's epilogue no longer reads them
-    if constexpr (!kRaw) store_scales();
+    if constexpr (!kRaw && !kDmaOnly) store_scales();
     if (S - 1 < cur_nk) issue(S - 1);
-    load_frags(0, 0, 0);
+    if constexpr (!kDmaOnly) load_frags(0, 0, 0);
 
     for (int kt = 0; kt < cur_nk; ++kt) {
 #pragma unroll
@@ -442,7 +466,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
         // burst of vector-memory issues while the matrix core idles.
         if (ks == 0 && kt > 0 && kt - 1 + S < cur_nk) issue(kt - 1 + S, C::kLPW / 2, C::kLPW);
         if (ks + 1 < kSub) {
-          load_frags(kt, ks + 1, cb ^ 1);
+          if constexpr (!kDmaOnly) load_frags(kt, ks + 1, cb ^ 1);
         } else if (kt + 1 < cur_nk) {
           // Every wave's reads of stage kt are complete (the wait above);
           // once all are past the barrier the slot of stage kt can take
@@ -450,9 +474,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
           wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 2 - kt));
           barrier();
           if (kt + S < cur_nk) issue(kt + S, 0, C::kLPW / 2);
-          load_frags(kt + 1, 0, cb ^ 1);
+          if constexpr (!kDmaOnly) load_frags(kt + 1, 0, cb ^ 1);
         }
-        if constexpr (kW8A8) {
+        if constexpr (kDmaOnly) {
+          // operand-delivery floor: the same DMA, waits and barriers, no arithmetic
+        } else if constexpr (kW8A8) {
 #pragma unroll
           for (int j = 0; j < C::FM; ++j) {
 #pragma unroll
@@ -466,10 +492,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
         } else {
 #pragma unroll
           for (int i = 0; i < C::FN; ++i) {
-            const u32x2 c0 = i8x4_to_16x4<T>(fa[cb][i][0]);
-            const u32x2 c1 = i8x4_to_16x4<T>(fa[cb][i][1]);
-            const u32x2 c2 = i8x4_to_16x4<T>(fa[cb][i][2]);
-            const u32x2 c3 = i8x4_to_16x4<T>(fa[cb][i][3]);
+            u32x2 c0, c1, c2, c3;
+            if constexpr (kDq) {
+              c0 = i8x4_dq_to_16x4<T>(fa[cb][i][0], dqs[i]);
+              c1 = i8x4_dq_to_16x4<T>(fa[cb][i][1], dqs[i]);
+              c2 = i8x4_dq_to_16x4<T>(fa[cb][i][2], dqs[i]);
+              c3 = i8x4_dq_to_16x4<T>(fa[cb][i][3], dqs[i]);
+            } else {
+              c0 = i8x4_to_16x4<T>(fa[cb][i][0]);
+              c1 = i8x4_to_16x4<T>(fa[cb][i][1]);
+              c2 = i8x4_to_16x4<T>(fa[cb][i][2]);
+              c3 = i8x4_to_16x4<T>(fa[cb][i][3]);
+            }
             const u32x4 alo = u32x4{c0.x, c0.y, c1.x, c1.y};
             const u32x4 ahi = u32x4{c2.x, c2.y, c3.x, c3.y};
 #pragma unroll
@@ -497,6 +531,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 
     // Every wave has consumed its last fragments: the ring is free.
     barrier();
+    TVQ_TL_MARK(2);
     // ---- next tile: start its operand stream before this tile's stores ----
     const int next = unit + (int)gridDim.x;
     const bool more = next < units;
@@ -507,7 +542,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 #pragma unroll
       for (int s = 0; s < S - 1; ++s)
         if (s < nk) issue(s);
-      if constexpr (!kRaw) load_scales(tm * BM, tn * BN);
+      if constexpr (!kRaw && !kDmaOnly) load_scales(tm * BM, tn * BN);
     }
 
     // ---- split-K fixup ------------------------------------------------------
@@ -567,6 +602,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       if (threadIdx.x == 0) __hip_atomic_exchange(cnt + cur_tl, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
+    if constexpr (!kDmaOnly) {
     // ---- epilogue -----------------------------------------------------------
     // MF 16: acc reg t -> n = 4g + t.  MF 32: reg v -> n = 8*(v/4) + 4g + v%4.
     // Either way a lane owns runs of 4 consecutive output channels of token r.
@@ -623,8 +659,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 #pragma unroll
       for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-        for (int q = 0; q < kQ; ++q) wsv[i][q] = *reinterpret_cast<const f32x4*>(sc_w + MF * i + 8 * q + 4 * g);
+        for (int q = 0; q < kQ; ++q)
+          wsv[i][q] = kDq ? f32x4{1.0f, 1.0f, 1.0f, 1.0f}
+                          : *reinterpret_cast<const f32x4*>(sc_w + MF * i + 8 * q + 4 * g);
       const bool has_bias = bias != nullptr;
+      TVQ_TL_MARK(4);
       auto epi_slices = [&](auto bias_c) {
         constexpr bool kBias = decltype(bias_c)::value;
 #pragma unroll
@@ -675,6 +714,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
           // LDS operations of one wave complete in order; the wait and the
           // compiler barrier keep the read-back after the writes above.
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          TVQ_TL_MARK(5);
 #pragma unroll
           for (int ps = 0; ps < kPass; ++ps) {
             const int e = ps * 64 + lane;
@@ -695,6 +735,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
             }
           }
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          TVQ_TL_MARK(6);
         }
       };
       if (has_bias)
@@ -702,8 +743,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       else
         epi_slices(std::false_type{});
     }
+    }
     if (!more) break;
   }
+  TVQ_TL_MARK(3);
 }
 
 // CU count of the current device (cached per device; 0 without a device).
@@ -743,12 +786,12 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false, bool kGlu = false, bool kRot = false>
+          bool kNtW = false, bool kGlu = false, bool kRot = false, bool kDmaOnly = false, bool kDq = false>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
                       int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
                       hipStream_t stream) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
-  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu, kRot>;
+  auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu, kRot, kDmaOnly, kDq>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

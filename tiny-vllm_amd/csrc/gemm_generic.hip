@@ -10,7 +10,7 @@
 namespace tvq {
 namespace {
 
-template <typename T, bool kW8A8, bool kRaw>
+template <typename T, bool kW8A8, bool kRaw, bool kDq = false>
 __global__ __launch_bounds__(256) void generic_kernel(const void* __restrict__ xv, const float* __restrict__ a_scales,
                                                       const int8_t* __restrict__ qw, const float* __restrict__ ws,
                                                       const uint16_t* __restrict__ bias, void* __restrict__ yv,
@@ -33,17 +33,23 @@ __global__ __launch_bounds__(256) void generic_kernel(const void* __restrict__ x
   } else {
     const uint16_t* x = static_cast<const uint16_t*>(xv) + m * K;
     float acc = 0.0f;
-    for (int64_t k = 0; k < K; ++k) acc = __builtin_fmaf(to_float<T>(x[k]), (float)w[k], acc);
+    if constexpr (kDq) {
+      // T(T(q) * T(s)) per weight (int8_weight_only_gemm.cu:401-411)
+      const float sr = round_to<T>(ws[n]);
+      for (int64_t k = 0; k < K; ++k) acc = __builtin_fmaf(to_float<T>(x[k]), round_to<T>((float)w[k] * sr), acc);
+    } else {
+      for (int64_t k = 0; k < K; ++k) acc = __builtin_fmaf(to_float<T>(x[k]), (float)w[k], acc);
+    }
     const float b = bias ? to_float<T>(bias[n]) : 0.0f;
-    static_cast<uint16_t*>(yv)[idx] = from_float<T>(epi_w8a16(acc, ws[n], b));
+    static_cast<uint16_t*>(yv)[idx] = from_float<T>(epi_w8a16(acc, kDq ? 1.0f : ws[n], b));
   }
 }
 
-template <typename T, bool kW8A8, bool kRaw>
+template <typename T, bool kW8A8, bool kRaw, bool kDq = false>
 hipError_t launch_t(const GemmArgs& a, hipStream_t stream) {
   const int64_t total = a.M * a.N;
   const dim3 grid((unsigned)((total + 255) / 256));
-  generic_kernel<T, kW8A8, kRaw><<<grid, dim3(256), 0, stream>>>(
+  generic_kernel<T, kW8A8, kRaw, kDq><<<grid, dim3(256), 0, stream>>>(
       a.x, a.a_scales, a.qweight, a.scales, static_cast<const uint16_t*>(a.bias), a.y, a.M, a.N, a.K);
   return hipGetLastError();
 }
@@ -56,6 +62,10 @@ hipError_t launch_generic(const GemmArgs& a, hipStream_t stream) {
     return a.bf16 ? launch_t<BF16, true, false>(a, stream) : launch_t<F16, true, false>(a, stream);
   }
   return a.bf16 ? launch_t<BF16, false, false>(a, stream) : launch_t<F16, false, false>(a, stream);
+}
+
+hipError_t launch_generic_dq(const GemmArgs& a, hipStream_t stream) {
+  return a.bf16 ? launch_t<BF16, false, false, true>(a, stream) : launch_t<F16, false, false, true>(a, stream);
 }
 
 }  // namespace tvq

@@ -82,6 +82,30 @@ __device__ __forceinline__ u32x2 i8x4_to_16x4<F16>(uint32_t w) {
   return r;
 }
 
+// Four signed int8 weights of one output channel, each multiplied by that
+// channel's scale already rounded to T (sr), rounded once more to T: the
+// element-wise T(T(q) * T(s)) of the reference's dequantization
+// (int8_weight_only_gemm.cu:401-411; cuda.py:293-300). T(q) * T(s) has at most
+// 8 + 11 significant bits, so the fp32 product is exact and the one RN
+// conversion equals the reference's rounded multiply.
+template <typename T>
+__device__ __forceinline__ u32x2 i8x4_dq_to_16x4(uint32_t w, float sr) {
+  const float f0 = (float)(int8_t)(w) * sr;
+  const float f1 = (float)(int8_t)(w >> 8) * sr;
+  const float f2 = (float)(int8_t)(w >> 16) * sr;
+  const float f3 = (float)((int32_t)w >> 24) * sr;
+  u32x2 r;
+  r.x = (uint32_t)from_float<T>(f0) | ((uint32_t)from_float<T>(f1) << 16);
+  r.y = (uint32_t)from_float<T>(f2) | ((uint32_t)from_float<T>(f3) << 16);
+  return r;
+}
+
+// The channel scale rounded to the activation type, as a float.
+template <typename T>
+__device__ __forceinline__ float round_to(float s) {
+  return to_float<T>(from_float<T>(s));
+}
+
 // One 16x16x32 MFMA on 16-bit operands held as four dwords (eight elements).
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);

@@ -62,6 +62,14 @@ hipError_t launch_tiled(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_generic(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_dma_gemm(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_dma_glu(const GemmArgs& a, hipStream_t stream);
+// The DMA tiling's operand stream alone (no arithmetic, no output): the
+// measurement floor of launch_dma_gemm for the same shape.
+hipError_t launch_dma_floor(const GemmArgs& a, hipStream_t stream);
+// W8A16 with each weight dequantized to T(T(q) * T(s)) before the dot product
+// (the reference kernel's rounding): DMA tiles when K % 128 == 0, else the
+// generic kernel.
+hipError_t launch_dma_dq(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_generic_dq(const GemmArgs& a, hipStream_t stream);
 bool dma_shape_ok(int64_t K);
 // Path name, with a "_splitk" suffix when a workspace of the given size makes
 // the launch split K (which needs the device: without one it never splits).

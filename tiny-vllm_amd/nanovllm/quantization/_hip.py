@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_NAME = "libtinyvllm_quant.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OP_ACT_QUANT = 0
 OP_W8A16 = 1
@@ -40,6 +40,8 @@ SYMBOLS = (
     ("tvq_w8a16_gemm", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _I64, _VP)),
     ("tvq_w8a8_gemm", _INT, (_VP, _VP, _VP, _VP, _VP, _VP, _INT, _I64, _I64, _I64, _VP, _I64, _VP)),
     ("tvq_w8a8_gemm_i32", _INT, (_VP, _VP, _VP, _I64, _I64, _I64, _VP, _I64, _VP)),
+    ("tvq_w8a16_gemm_rounded", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP)),
+    ("tvq_gemm_operand_floor", _INT, (_INT, _VP, _VP, _I64, _I64, _I64, _VP)),
     ("tvq_w8a8_linear", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _I64, _VP)),
     ("tvq_gemm_workspace_bytes", _I64, ()),
     ("tvq_w8a8_linear_noalloc", _INT, (_VP, _INT, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP)),
@@ -217,6 +219,38 @@ def w8a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                                 _ptr(bias), y.data_ptr(), m, n, k, *_ws(dev, split_k), _stream(dev))
     _check(rc, "tvq_w8a16_gemm")
     return y
+
+
+def w8a16_gemm_rounded(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+                       bias: torch.Tensor | None = None) -> torch.Tensor:
+    """W8A16 with the reference kernel's rounding: y = x @ wd^T + bias with
+    wd = T(T(qweight) * T(scales)[:,None]) in the activation dtype T."""
+    lib = load_library()
+    dev = _require_gpu(x, qweight, scales, bias)
+    _require(x.dim() == 2, "x must be 2-D")
+    _require(x.dtype in _TORCH_TO_TVQ, "x must be float16 or bfloat16")
+    m, k = x.shape
+    n = _check_weight(qweight, scales, bias, k, x.dtype)
+    y = torch.empty((m, n), dtype=x.dtype, device=dev)
+    if m == 0:
+        return y
+    with torch.cuda.device(dev):
+        rc = lib.tvq_w8a16_gemm_rounded(x.data_ptr(), _TORCH_TO_TVQ[x.dtype], qweight.data_ptr(), scales.data_ptr(),
+                                        _ptr(bias), y.data_ptr(), m, n, k, _stream(dev))
+    _check(rc, "tvq_w8a16_gemm_rounded")
+    return y
+
+
+def gemm_operand_floor(op: int, x: torch.Tensor, qweight: torch.Tensor) -> None:
+    """Measurement: the operand stream alone of the DMA GEMM tiles the library
+    would launch for (op, x, qweight); writes nothing."""
+    lib = load_library()
+    dev = _require_gpu(x, qweight)
+    m, k = x.shape
+    n = qweight.shape[0]
+    with torch.cuda.device(dev):
+        rc = lib.tvq_gemm_operand_floor(op, x.data_ptr(), qweight.data_ptr(), m, n, k, _stream(dev))
+    _check(rc, "tvq_gemm_operand_floor")
 
 
 def w8a8_gemm(x_q: torch.Tensor, a_scales: torch.Tensor, qweight: torch.Tensor, w_scales: torch.Tensor,

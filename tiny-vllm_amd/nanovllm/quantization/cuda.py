@@ -19,6 +19,13 @@ and the torch path computes the result. Two deliberate differences:
 * A missing or unloadable HIP library always raises (it is a broken install,
   not a per-call condition), so a GPU deployment can never run on the slower
   torch path without noticing.
+
+W8A16 numerics: by default the native kernels apply each channel's fp32 scale
+once per output, after the dot product. `NANOVLLM_INT8_DEQUANT_ROUNDING=reference`
+selects the reference kernel's rounding instead: every weight is dequantized to
+the activation dtype as dtype(dtype(q) * dtype(s)) before the dot product
+(int8_weight_only_gemm.cu:401-411, the same expression as the torch path,
+cuda.py:293-300). No reference counterpart as a switch.
 """
 from __future__ import annotations
 
@@ -59,6 +66,11 @@ def _get_w8a8_backend_preference() -> str:
 def _strict_native() -> bool:
     """NANOVLLM_NATIVE_STRICT: re-raise native failures instead of falling back."""
     return os.environ.get("NANOVLLM_NATIVE_STRICT", "").strip().lower() not in _OFF_VALUES
+
+
+def _rounded_dequant() -> bool:
+    """NANOVLLM_INT8_DEQUANT_ROUNDING=reference: the reference kernel's per-weight rounding."""
+    return os.environ.get("NANOVLLM_INT8_DEQUANT_ROUNDING", "fp32").strip().lower() in ("reference", "activation")
 
 
 def _get_phase() -> str:
@@ -122,9 +134,14 @@ def native_int8_weight_only_linear(x: torch.Tensor, qweight: torch.Tensor, scale
         raise RuntimeError("native INT8 weight-only backend requires GPU tensors")
     n = qweight.shape[0]
     x_2d = x.contiguous().view(-1, x.shape[-1])
+    bias = None if bias is None else bias.contiguous()
+    if _rounded_dequant():
+        _log_backend_event_once(backend="native", phase=_get_phase(), path="rounded_dequant", x=x_2d,
+                                qweight=qweight)
+        y = _hip.w8a16_gemm_rounded(x_2d, qweight.contiguous(), scales.contiguous(), bias)
+        return y.view(*x.shape[:-1], n)
     path = _hip.select_path(_hip.OP_W8A16, x_2d.shape[0], n, x_2d.shape[1], x.dtype)
     _log_backend_event_once(backend="native", phase=_get_phase(), path=path, x=x_2d, qweight=qweight)
-    bias = None if bias is None else bias.contiguous()
     y = _hip.w8a16_gemm(x_2d, qweight.contiguous(), scales.contiguous(), bias)
     return y.view(*x.shape[:-1], n)
 
