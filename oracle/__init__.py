@@ -21,7 +21,7 @@ Parity status per function (see tests/test_oracle.py):
   w8a8_torch_path          pinned against the exact fp64 product (bound)
   w8a16_f64 / w8a8_f64     pinned (brute force on tiny inputs, C vs numpy)
   w8a16_rounded_weights    pinned (CPU torch running the reference's expression,
-                           bit for bit; power-of-two scales; zero codes)
+                           bit for bit; power-of-two scales; known answers; C)
 """
 from __future__ import annotations
 
@@ -127,8 +127,9 @@ def w8a16_rounded_weights(q: np.ndarray, s: np.ndarray, is_bf16: bool = True) ->
         sr = bf16_bits_to_f32(f32_to_bf16_bits(s.astype(np.float32)))
         prod = (q.astype(np.float32) * sr[:, None]).astype(np.float32)
         return bf16_bits_to_f32(f32_to_bf16_bits(prod))
-    sr = s.astype(np.float16).astype(np.float32)
-    return (q.astype(np.float32) * sr[:, None]).astype(np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):  # overflow to +-inf is the IEEE result
+        sr = s.astype(np.float16).astype(np.float32)
+        return (q.astype(np.float32) * sr[:, None]).astype(np.float16).astype(np.float32)
 
 
 def w8a16_rounded_f64(x_f32: np.ndarray, wd_f32: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
@@ -245,8 +246,11 @@ _C = None
 
 
 def build_c(force: bool = False) -> Path:
-    """Compile tvq_oracle.c with the committed Makefile."""
-    if force or not LIB_PATH.is_file():
+    """Compile tvq_oracle.c with the committed Makefile (also when the built
+    library is older than the source)."""
+    src = ORACLE_DIR / "tvq_oracle.c"
+    stale = LIB_PATH.is_file() and LIB_PATH.stat().st_mtime < src.stat().st_mtime
+    if force or stale or not LIB_PATH.is_file():
         cmd = ["make", "-C", str(ORACLE_DIR)] + (["-B"] if force else [])
         subprocess.run(cmd, check=True, capture_output=True)
     return LIB_PATH
@@ -264,8 +268,11 @@ def c_lib() -> ctypes.CDLL:
         lib.oracle_w8a8_epilogue.argtypes = [vp, vp, vp, vp, i64, i64, vp, vp]
         lib.oracle_w8a16_f64.argtypes = [vp, i32, vp, vp, vp, i64, i64, i64, vp]
         lib.oracle_f32_to_bf16.argtypes = [vp, i64, vp]
+        lib.oracle_w8a16_rounded_weights.argtypes = [vp, vp, i32, i64, i64, vp]
+        lib.oracle_f32_to_f16.argtypes = [vp, i64, vp]
         for f in (lib.oracle_act_quant, lib.oracle_quant_f32, lib.oracle_gemm_i32, lib.oracle_w8a8_epilogue,
-                  lib.oracle_w8a16_f64, lib.oracle_f32_to_bf16):
+                  lib.oracle_w8a16_f64, lib.oracle_f32_to_bf16, lib.oracle_w8a16_rounded_weights,
+                  lib.oracle_f32_to_f16):
             f.restype = None
         _C = lib
     return _C
@@ -331,6 +338,23 @@ def c_w8a16_f64(x_bits: np.ndarray, q: np.ndarray, s: np.ndarray, bias_f32: np.n
     y = np.empty((m, n), np.float64)
     c_lib().oracle_w8a16_f64(_p(x_bits), int(is_bf16), _p(q), _p(s), _p(bias_f32), m, n, k, _p(y))
     return y
+
+
+def c_w8a16_rounded_weights(q: np.ndarray, s: np.ndarray, is_bf16: bool = True) -> np.ndarray:
+    """C restatement of w8a16_rounded_weights: the T bits of T(T(q) * T(s))."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    n, k = q.shape
+    out = np.empty((n, k), np.uint16)
+    c_lib().oracle_w8a16_rounded_weights(_p(q), _p(s), int(is_bf16), n, k, _p(out))
+    return out
+
+
+def c_f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    c_lib().oracle_f32_to_f16(_p(x), x.size, _p(out))
+    return out
 
 
 def c_f32_to_bf16(x: np.ndarray) -> np.ndarray:

@@ -145,6 +145,45 @@ void oracle_w8a16_f64(const uint16_t* x, int is_bf16, const int8_t* q, const flo
   }
 }
 
+/* Round-to-nearest-even float -> IEEE half (subnormals, overflow to inf). */
+static uint16_t f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00u;            /* NaN */
+  if (a >= 0x477ff000u) return sign | 0x7c00u;           /* >= 65520 rounds to inf */
+  if (a < 0x38800000u) {                                  /* below 2^-14: subnormal half */
+    float mag;
+    memcpy(&mag, &a, 4);
+    return sign | (uint16_t)nearbyintf(mag * 16777216.0f);  /* mag / 2^-24, exact scaling */
+  }
+  const uint32_t mant = a & 0x7fffffu;
+  uint32_t r = ((((a >> 23) - 127u + 15u) << 10) | (mant >> 13));
+  const uint32_t rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r += 1u;
+  return sign | (uint16_t)r;
+}
+
+/* The reference kernel's dequantized weight T(T(q) * T(s)) as T bits
+ * (int8_weight_only_gemm.cu:401-411; cuda.py:293-300): T(q) exact, T(s) by
+ * RNE, the product exact in float (<= 8 + 11 significant bits), one RNE. */
+void oracle_w8a16_rounded_weights(const int8_t* q, const float* s, int is_bf16, int64_t N, int64_t K,
+                                  uint16_t* wd) {
+  for (int64_t n = 0; n < N; ++n) {
+    const float sr = is_bf16 ? bf16_to_f32(f32_to_bf16(s[n])) : f16_to_f32(f32_to_f16(s[n]));
+    for (int64_t k = 0; k < K; ++k) {
+      const float p = (float)q[n * K + k] * sr;
+      wd[n * K + k] = is_bf16 ? f32_to_bf16(p) : f32_to_f16(p);
+    }
+  }
+}
+
+/* float -> half RNE over an array (exposed so the tests can pin it). */
+void oracle_f32_to_f16(const float* x, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(x[i]);
+}
+
 /* float -> bf16 RNE over an array (exposed so the tests can pin it). */
 void oracle_f32_to_bf16(const float* x, int64_t n, uint16_t* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(x[i]);

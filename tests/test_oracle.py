@@ -451,3 +451,33 @@ def test_rounded_f64_brute_force_tiny():
         for n in range(4):
             assert y[m, n] == pytest.approx(sum(float(x[m, k]) * float(wd[n, k]) for k in range(7)) + float(b[n]),
                                             rel=1e-15, abs=1e-15)
+
+
+@pytest.mark.parametrize("is_bf16", [True, False])
+def test_rounded_weights_c_matches_numpy(is_bf16):
+    """The two restatements of the rounded dequantization agree bit for bit."""
+    rng = np.random.default_rng(21)
+    q = rng.integers(-127, 128, size=(96, 255), dtype=np.int8)
+    q[:, :255] = np.tile(np.arange(-127, 128, dtype=np.int8), (96, 1))
+    s = (rng.random(96) * 10.0 ** rng.integers(-6, 1, size=96)).astype(np.float32)
+    s[:4] = np.float32([2.0 ** -12, 1.0 / 3.0, 65504.0 / 127.0, 1e-7])
+    bits = oracle.c_w8a16_rounded_weights(q, s, is_bf16=is_bf16)
+    got = oracle.to_f32(bits, is_bf16)
+    want = oracle.w8a16_rounded_weights(q, s, is_bf16=is_bf16)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_c_f16_rounding_matches_numpy():
+    """The C float -> half RNE (used by the rounded-dequant restatement) equals
+    numpy's conversion on random values across the half range, the subnormal
+    range, exact ties and overflow."""
+    rng = np.random.default_rng(8)
+    x = np.concatenate([
+        (rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 5, size=20000)).astype(np.float32),
+        np.float32([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26,
+                    2.0 ** -14, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, np.inf, -np.inf]),
+    ])
+    got = oracle.c_f32_to_f16(x)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
