@@ -32,7 +32,7 @@ def test_header_declares_expected_entry_points():
     syms = _declared_symbols()
     for name in ("tvq_abi_version", "tvq_last_error", "tvq_select_path", "tvq_act_quant", "tvq_w8a16_gemm",
                  "tvq_w8a8_gemm", "tvq_w8a8_gemm_i32", "tvq_w8a8_linear", "tvq_rmsnorm", "tvq_silu_mul",
-                 "tvq_gemm_workspace_bytes"):
+                 "tvq_gemm_workspace_bytes", "tvq_w8a16_gemm_rounded", "tvq_gemm_operand_floor"):
         assert name in syms
 
 
@@ -58,6 +58,19 @@ def test_abi_version_and_errors_without_gpu(hiplib):
     assert hiplib.tvq_w8a8_gemm_i32(None, None, None, 1, 1, 1 << 40, None, 0, None) == -2
     assert b"2^31" in hiplib.tvq_last_error()
     assert hiplib.tvq_act_quant(None, 1, 4, 16, -1.0, None, None, None) == -1
+    # rounded-dequant W8A16: same validation as tvq_w8a16_gemm
+    assert hiplib.tvq_w8a16_gemm_rounded(None, 9, None, None, None, None, 1, 1, 16, None) == -1
+    assert b"dtype" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a16_gemm_rounded(None, 1, None, None, None, None, 1, 1, 16, None) == -1
+    assert b"null pointer" in hiplib.tvq_last_error()
+    assert hiplib.tvq_w8a16_gemm_rounded(None, 1, None, None, None, None, 0, 8, 16, None) == 0
+    # operand floor: op check, then the DMA tiles' shape rule, before any launch
+    assert hiplib.tvq_gemm_operand_floor(0, 0x1000, 0x1000, 4, 8, 128, None) == -1
+    assert b"op must be" in hiplib.tvq_last_error()
+    assert hiplib.tvq_gemm_operand_floor(2, 0x1000, 0x1000, 4, 8, 96, None) == -2
+    assert b"K % 128" in hiplib.tvq_last_error()
+    assert hiplib.tvq_gemm_operand_floor(1, 0x1008, 0x1000, 4, 8, 128, None) == -2
+    assert hiplib.tvq_gemm_operand_floor(2, None, 0x1000, 4, 8, 128, None) == -1
     assert hiplib.tvq_rmsnorm(None, None, None, 1e-6, None, None, None, 1, 4, 16, None) == -1
     assert b"null pointer" in hiplib.tvq_last_error()
     assert hiplib.tvq_rmsnorm(1, None, 1, 1e-6, None, None, None, 1, 4, 16, None) == -1
@@ -344,3 +357,14 @@ def test_noalloc_linear_rejects_sizes_beyond_its_scratch(hiplib):
     rc = hiplib.tvq_w8a8_linear_noalloc(None, 1, None, None, None, None, 65537, 64, 16, None)
     assert rc == -2
     assert hiplib.tvq_w8a8_linear_noalloc(None, 1, None, None, None, None, -1, 64, 16, None) == -1
+
+
+def test_rounded_dequant_switch(monkeypatch):
+    """NANOVLLM_INT8_DEQUANT_ROUNDING selects the reference kernel's rounding
+    only for 'reference' / 'activation'; anything else keeps the fp32 scale."""
+    from nanovllm.quantization import cuda
+    for value, want in (("reference", True), ("Activation", True), ("fp32", False), ("", False), ("bf16x", False)):
+        monkeypatch.setenv("NANOVLLM_INT8_DEQUANT_ROUNDING", value)
+        assert cuda._rounded_dequant() is want
+    monkeypatch.delenv("NANOVLLM_INT8_DEQUANT_ROUNDING")
+    assert cuda._rounded_dequant() is False
