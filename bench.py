@@ -16,7 +16,9 @@ timed step reads its weights from HBM at any --steps.
 
 Extra keys on the same line:
   roofline      the dominant kernel (the W8A8 GEMM) timed with HIP events on
-                its launch stream: algorithmic bytes / average launch time
+                its launch stream: algorithmic bytes / average launch time;
+                operand_floor_us is the same tiles' operand stream alone
+                (tvq_gemm_operand_floor), the floor its data movement sets
   cpu_baseline  the reference's torch path (quantize -> dequantize -> F.linear)
                 restated in CPU torch, timed on this host's cores
   targets       the three north-star targets, from the sweep and the E2E leg
@@ -24,7 +26,8 @@ Extra keys on the same line:
                 W8A16 vs W8A8 prefill / decode tok/s and TTFT (run first, in a
                 child process, before this process touches the GPU)
   sweep         configs 1-4, one compact entry per (mode, shape, M):
-                "cfg mode MxNxK path us frac" (full records: gpurun_out/bench_sweep.jsonl)
+                "cfg mode MxNxK path us frac [floorF us] [aqA us]" (full records:
+                bench_sweep.jsonl in the output folder)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--no-e2e]
 """
