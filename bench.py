@@ -257,8 +257,11 @@ def run_sweep(lib, dev, quick=False):
             # operand-delivery floor of the same tiles (unsplit), same weight copies
             op = _hip.OP_W8A8 if mode == "w8a8" else _hip.OP_W8A16
             xa = xq if mode == "w8a8" else x
-            tf = time_kernel(lambda i: L.operand_floor(op, xa, qs[i]), copies)
-            rec["floor_us"] = round(tf * 1e6, 3)
+            try:
+                tf = time_kernel(lambda i: L.operand_floor(op, xa, qs[i]), copies)
+                rec["floor_us"] = round(tf * 1e6, 3)
+            except RuntimeError as exc:
+                print(f"operand floor not measured for {tag} {mode} {m}x{n}x{k}: {exc}", file=sys.stderr)
         if tq is not None:
             rec["act_quant_us"] = round(tq * 1e6, 3)
             rec["act_quant_gbs"] = round(act_quant_bytes(m, k) / tq / 1e9, 1)
@@ -484,12 +487,17 @@ def main():
             traffic = rec.get("hbm_bytes_per_launch")
     # The same tiles' operand stream alone (no MFMA, no output): the floor that
     # the GEMM's data movement sets, over the same rotating weight copies.
-    t_floor = time_kernel(lambda i: L.operand_floor(_hip.OP_W8A8, xq0, qs[i]), copies, min_launches=256)
+    try:
+        t_floor = time_kernel(lambda i: L.operand_floor(_hip.OP_W8A8, xq0, qs[i]), copies, min_launches=256)
+    except RuntimeError as exc:  # auxiliary: the headline line must not depend on it
+        print(f"operand floor not measured: {exc}", file=sys.stderr)
+        t_floor = None
     roof = dict(bound=r["bound"], achieved=round(r["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
                 frac=round(r["gbs"] / PEAK_HBM_GBS, 4), traffic=traffic,
                 kernel=_hip.select_path(_hip.OP_W8A8, m, n, k), kernel_us=round(t_gemm * 1e6, 3),
                 algorithmic_bytes=r["bytes"], tops=round(r["tops"], 3),
-                operand_floor_us=round(t_floor * 1e6, 3), floor_over_kernel=round(t_floor / t_gemm, 4))
+                operand_floor_us=None if t_floor is None else round(t_floor * 1e6, 3),
+                floor_over_kernel=None if t_floor is None else round(t_floor / t_gemm, 4))
     del x, qs, ss
     torch.cuda.empty_cache()
 
