@@ -28,6 +28,8 @@
 // idle with whole-K tiles (e.g. 64 tiles of 64x64 for N = 4096), so with a
 // caller workspace they split K into up to CUs/tiles ranges of >= 8 stages,
 // one work unit per CU (e.g. 8B down_proj at M = 64: 49 -> 22 us W8A16).
+#include <stdlib.h>
+
 #include "gemm_dma_kernel.h"
 #include "tvq_internal.h"
 
@@ -46,18 +48,29 @@ struct CfgInfo {
   int bm, bn, wm, wn, s, mf, ks;  // ks: k values per ring stage
   const char* name;
   const char* name_split;  // the same tiles with K split over several workgroups
+  const char* name_streamk;  // the same tiles with stream-K (equal k-stage shares per CU)
 };
 constexpr CfgInfo kInfo[] = {
-    {true, 256, 256, 2, 4, 2, 32, 128, "dma_mfma_i8_256x256", "dma_mfma_i8_256x256_splitk"},
-    {true, 256, 128, 4, 2, 3, 32, 128, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk"},
-    {true, 64, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_64x64", "dma_mfma_i8_64x64_splitk"},
-    {true, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_i8_64x128", "dma_mfma_i8_64x128_splitk"},
-    {true, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_32x64", "dma_mfma_i8_32x64_splitk"},
-    {false, 128, 256, 2, 4, 2, 32, 128, "dma_mfma_f16x_128x256", "dma_mfma_f16x_128x256_splitk"},
-    {false, 64, 128, 2, 2, 4, 32, 128, "dma_mfma_f16x_64x128", "dma_mfma_f16x_64x128_splitk"},
-    {false, 64, 64, 2, 2, 4, 32, 128, "dma_mfma_f16x_64x64", "dma_mfma_f16x_64x64_splitk"},
-    {false, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_f16x_32x64", "dma_mfma_f16x_32x64_splitk"},
-    {false, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_f16x_64x128w8", "dma_mfma_f16x_64x128w8_splitk"},
+    {true, 256, 256, 2, 4, 2, 32, 128, "dma_mfma_i8_256x256", "dma_mfma_i8_256x256_splitk",
+     "dma_mfma_i8_256x256_streamk"},
+    {true, 256, 128, 4, 2, 3, 32, 128, "dma_mfma_i8_256x128", "dma_mfma_i8_256x128_splitk",
+     "dma_mfma_i8_256x128_streamk"},
+    {true, 64, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_64x64", "dma_mfma_i8_64x64_splitk",
+     "dma_mfma_i8_64x64_streamk"},
+    {true, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_i8_64x128", "dma_mfma_i8_64x128_splitk",
+     "dma_mfma_i8_64x128_streamk"},
+    {true, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_i8_32x64", "dma_mfma_i8_32x64_splitk",
+     "dma_mfma_i8_32x64_streamk"},
+    {false, 128, 256, 2, 4, 2, 32, 128, "dma_mfma_f16x_128x256", "dma_mfma_f16x_128x256_splitk",
+     "dma_mfma_f16x_128x256_streamk"},
+    {false, 64, 128, 2, 2, 4, 32, 128, "dma_mfma_f16x_64x128", "dma_mfma_f16x_64x128_splitk",
+     "dma_mfma_f16x_64x128_streamk"},
+    {false, 64, 64, 2, 2, 4, 32, 128, "dma_mfma_f16x_64x64", "dma_mfma_f16x_64x64_splitk",
+     "dma_mfma_f16x_64x64_streamk"},
+    {false, 32, 64, 2, 2, 4, 16, 128, "dma_mfma_f16x_32x64", "dma_mfma_f16x_32x64_splitk",
+     "dma_mfma_f16x_32x64_streamk"},
+    {false, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_f16x_64x128w8", "dma_mfma_f16x_64x128w8_splitk",
+     "dma_mfma_f16x_64x128w8_streamk"},
 };
 
 static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_64x128w8 + 1, "one entry per DmaCfg");
@@ -82,7 +95,22 @@ int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm)
 // workspace): M <= 64, fewer than 16384 output channels, K >= 2048.
 bool split_shape(int64_t M, int64_t N, int64_t K) { return M <= 64 && N < 16384 && K >= 2048; }
 
+// Stream-K for decode-size M (TVQ_STREAMK=1; read per call): every CU takes
+// an equal share of the tiles' k-stages (gemm_dma_kernel.h), so shapes whose
+// tile count is not a multiple of the CU count (e.g. 192 tiles of 64x128 on
+// 256 CUs at the 8B gate_up) keep every CU's weight stream busy. It needs a
+// workspace of two accumulator images per workgroup.
+bool streamk_shape(int64_t M) {
+  const char* env = getenv("TVQ_STREAMK");
+  return M <= 64 && env != nullptr && env[0] == '1';
+}
+
 DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
+  if (streamk_shape(M)) {
+    // the widest decode tiles: activation traffic per weight byte 2M/BN (W8A16), M/BN (W8A8)
+    if (w8a8) return M > 32 ? DmaCfg::kI8_64x128 : DmaCfg::kI8_32x64;
+    return M > 32 ? DmaCfg::kH_64x128w8 : DmaCfg::kH_32x64;
+  }
   const bool split = split_shape(M, N, K);
   if (w8a8) {
     if (tiles(M, N, 256, 256) >= 256) return DmaCfg::kI8_256x256;
@@ -112,6 +140,20 @@ int m_major(const GemmArgs& a) {
   return a.N * a.K > xbytes ? 1 : 0;
 }
 
+// Stream-K range length for configuration c (0: no stream-K launch).
+template <DmaCfg c>
+int streamk_len(int64_t M, int64_t N, int64_t K, const void* ws, int64_t ws_bytes) {
+  if constexpr (!splittable<c>()) {
+    return 0;
+  } else {
+    if (!streamk_shape(M)) return 0;
+    constexpr CfgInfo i = info<c>();
+    int grid = 0;
+    return dma::choose_streamk((int)tiles(M, N, i.bm, i.bn), (int)(K / i.ks), dma::device_cus(), i.bm * i.bn * 4, ws,
+                               ws_bytes, &grid);
+  }
+}
+
 template <DmaCfg c>
 int splits_of(int64_t M, int64_t N, int64_t K, const void* ws, int64_t ws_bytes) {
   if constexpr (!splittable<c>()) {
@@ -135,6 +177,17 @@ int splits_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64_
   return 1;
 }
 
+int streamk_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64_t ws_bytes) {
+  switch (c) {
+#define TVQ_CASE(C) \
+  case DmaCfg::C: return streamk_len<DmaCfg::C>(M, N, K, ws, ws_bytes);
+    TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
+    TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
+#undef TVQ_CASE
+  }
+  return 0;
+}
+
 template <typename T, bool kRaw, DmaCfg c>
 hipError_t go(const GemmArgs& a, hipStream_t s) {
   constexpr CfgInfo i = info<c>();
@@ -142,6 +195,10 @@ hipError_t go(const GemmArgs& a, hipStream_t s) {
   // Unsplit launches use the instantiation without the split-K fixup (fewer
   // registers; measured ~4 % faster on the M=256 headline shape).
   if constexpr (splittable<c>()) {
+    if (streamk_for(c, a.M, a.N, a.K, a.workspace, a.workspace_bytes) > 0)
+      return launch_dma<T, i.w8a8, kRaw, i.bm, i.bn, i.wm, i.wn, i.s, i.mf, i.ks, true, i.w8a8, false, false, false,
+                        false, true>(a.x, a.a_scales, a.qweight, a.scales, a.bias, a.y, (int)a.M, (int)a.N, (int)a.K,
+                                     8, m_major(a), 1, a.workspace, a.workspace_bytes, s);
     // W8A8 at decode-size M (<= 64, one or two m-tiles): each weight byte is
     // read by at most two workgroups, so the weight stream takes the
     // non-temporal hint
@@ -195,7 +252,10 @@ int dma_splits(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_byt
 }
 
 const char* dma_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes) {
-  const CfgInfo& i = kInfo[(int)choose(w8a8, M, N, K)];
+  static char probe;
+  const DmaCfg c = choose(w8a8, M, N, K);
+  const CfgInfo& i = kInfo[(int)c];
+  if (streamk_for(c, M, N, K, workspace_bytes > 0 ? &probe : nullptr, workspace_bytes) > 0) return i.name_streamk;
   return dma_splits(w8a8, M, N, K, workspace_bytes) > 1 ? i.name_split : i.name;
 }
 

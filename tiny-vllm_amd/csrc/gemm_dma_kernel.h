@@ -238,7 +238,8 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 }
 
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false, bool kGlu = false, bool kRot = false, bool kDmaOnly = false, bool kDq = false>
+          bool kNtW = false, bool kGlu = false, bool kRot = false, bool kDmaOnly = false, bool kDq = false,
+          bool kSK = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __restrict__ xv,
                                                                 const float* __restrict__ a_scales,
                                                                 const int8_t* __restrict__ qw,
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
                                                                 const uint16_t* __restrict__ bias,
                                                                 void* __restrict__ yv, int M, int N, int K,
                                                                 int group, int m_major, int splits,
-                                                                char* __restrict__ wsp) {
+                                                                char* __restrict__ wsp, int sk_len) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
   using Acc = typename std::conditional<
       MF == 32, typename std::conditional<kW8A8, i32x16, f32x16>::type,
@@ -273,6 +274,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     kb_ = sk_ * nk_per;
     kn_ = max(0, min(nk_all, kb_ + nk_per) - kb_);
   };
+  // Stream-K (sk_len > 0): the tiles' k-stages form one sequence, tile-major
+  // (tile t owns positions t*nk_all .. t*nk_all + nk_all - 1), and workgroup w
+  // owns positions [w*sk_len, (w+1)*sk_len). Its range cuts into segments at
+  // tile boundaries; only its first and last segment can be part of a tile.
+  static_assert(!kSK || kSplit, "stream-K uses the split-K fixup");
+  constexpr bool streamk = kSK;
+  int sk_pos = (int)blockIdx.x * sk_len;
+  const int sk_end = streamk ? min(total * nk_all, sk_pos + sk_len) : 0;
+  auto seg_coords = [&](int& tm_, int& tn_, int& tl_, int& kb_, int& kn_) {
+    tl_ = sk_pos / nk_all;
+    kb_ = sk_pos - tl_ * nk_all;
+    kn_ = min(nk_all - kb_, sk_end - sk_pos);
+    tile_coords(tl_, tiles_m, tiles_n, group, m_major, tm_, tn_);
+  };
+  if (streamk && sk_pos >= sk_end) return;  // (the host sizes the grid so that this never happens)
 
   // ---- per-lane DMA sources for this wave's blocks ----------------------
   // Each source is a wave-uniform tile base (scalar registers) plus a 32-bit
@@ -393,7 +409,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   TVQ_TL_MARK(0);
   int unit = blockIdx.x;
   int tm, tn, tl, sk, kb, nk;
-  unit_coords(unit, tm, tn, tl, sk, kb, nk);
+  if (streamk) {
+    sk = 0;  // stream-K: 0 while in the workgroup's first segment, 1 after it
+    seg_coords(tm, tn, tl, kb, nk);
+  } else {
+    unit_coords(unit, tm, tn, tl, sk, kb, nk);
+  }
   set_sources(tm * BM, tn * BN, kb, nk, tm + tn);
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
@@ -533,11 +554,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     barrier();
     TVQ_TL_MARK(2);
     // ---- next tile: start its operand stream before this tile's stores ----
-    const int next = unit + (int)gridDim.x;
-    const bool more = next < units;
+    bool more;
+    if (streamk) {
+      sk_pos += cur_nk;
+      more = sk_pos < sk_end;
+    } else {
+      more = unit + (int)gridDim.x < units;
+    }
     if (more) {
-      unit = next;
-      unit_coords(unit, tm, tn, tl, sk, kb, nk);
+      if (streamk) {
+        sk = 1;
+        seg_coords(tm, tn, tl, kb, nk);
+      } else {
+        unit += (int)gridDim.x;
+        unit_coords(unit, tm, tn, tl, sk, kb, nk);
+      }
       set_sources(tm * BM, tn * BN, kb, nk, tm + tn);
 #pragma unroll
       for (int s = 0; s < S - 1; ++s)
@@ -550,19 +581,34 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     // and loads, which bypass the per-XCD L2 and meet at the coherent memory
     // side; so completing the stores (vmcnt 0) before the counter update is
     // the whole release, and no L2 write-back or invalidate is needed.
-    if (kSplit && splits > 1) {
+    // Stream-K: the workgroups w0..w1 whose ranges meet this tile contribute
+    // to it, in k order. Contributor w's image is image 2w when the tile is
+    // its first segment (every contributor after w0, and w0 when its range
+    // starts inside the tile), else 2w + 1 (its last segment).
+    int sk_w0 = 0, sk_parts = splits;
+    if (streamk) {
+      sk_w0 = cur_tl * nk_all / sk_len;
+      sk_parts = ((cur_tl + 1) * nk_all - 1) / sk_len - sk_w0 + 1;
+    }
+    if (kSplit && sk_parts > 1) {
       using E = typename std::conditional<kW8A8, int32_t, float>::type;
       constexpr int kQ4 = kAccN / 4;
       E* part = reinterpret_cast<E*>(wsp + kSplitCntBytes);
       int* cnt = reinterpret_cast<int*>(wsp);
       int* last_flag = reinterpret_cast<int*>(smem + C::kRingBytes + C::kScN * 4);
+      // Image index of contribution s (0 .. sk_parts-1, in k order) to this tile.
+      auto img_index = [&](int s) -> int64_t {
+        if (!streamk) return (int64_t)cur_tl * splits + s;
+        const int w = sk_w0 + s;
+        return 2 * (int64_t)w + ((int64_t)w * sk_len >= (int64_t)cur_tl * nk_all ? 0 : 1);
+      };
       // Register image: value e of 4-value group q of fragment (i, j) of this
       // wave at (((wave * FN + i) * FM + j) * kQ4 + q) * 256 + 64 * e + lane,
       // so each store instruction of a wave covers 256 contiguous bytes.
-      auto img = [&](int s, int i, int j, int q, int e) {
-        return part + ((int64_t)cur_tl * splits + s) * (BM * BN) + (((wave * C::FN + i) * C::FM + j) * kQ4 + q) * 256 +
-               64 * e + lane;
+      auto img = [&](int64_t idx, int i, int j, int q, int e) {
+        return part + idx * (BM * BN) + (((wave * C::FN + i) * C::FM + j) * kQ4 + q) * 256 + 64 * e + lane;
       };
+      const int64_t own = streamk ? 2 * (int64_t)blockIdx.x + cur_sk : img_index(cur_sk);
 #pragma unroll
       for (int i = 0; i < C::FN; ++i)
 #pragma unroll
@@ -571,12 +617,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
           for (int q = 0; q < kQ4; ++q)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              __hip_atomic_store(img(cur_sk, i, j, q, e), (E)acc[i][j][4 * q + e], __ATOMIC_RELAXED,
+              __hip_atomic_store(img(own, i, j, q, e), (E)acc[i][j][4 * q + e], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
       wait_vm<0>();
       __syncthreads();
       if (threadIdx.x == 0)
-        *last_flag = __hip_atomic_fetch_add(cnt + cur_tl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+        *last_flag =
+            __hip_atomic_fetch_add(cnt + cur_tl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sk_parts - 1;
       __syncthreads();
       if (!*last_flag) {
         if (!more) break;
@@ -588,7 +635,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       for (int i = 0; i < C::FN; ++i)
 #pragma unroll
         for (int j = 0; j < C::FM; ++j) acc[i][j] = Acc{};
-      for (int s = 0; s < splits; ++s) {
+      for (int s = 0; s < sk_parts; ++s) {
+        const int64_t idx = img_index(s);
 #pragma unroll
         for (int i = 0; i < C::FN; ++i)
 #pragma unroll
@@ -597,7 +645,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
             for (int q = 0; q < kQ4; ++q)
 #pragma unroll
               for (int e = 0; e < 4; ++e)
-                acc[i][j][4 * q + e] += __hip_atomic_load(img(s, i, j, q, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                acc[i][j][4 * q + e] += __hip_atomic_load(img(idx, i, j, q, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (threadIdx.x == 0) __hip_atomic_exchange(cnt + cur_tl, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -785,12 +833,53 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
   return (nk + per - 1) / per;
 }
 
+// Stream-K range length (tile-stages per workgroup) for `tiles` tiles of `nk`
+// k-stages on `cus` CUs: one workgroup per CU, each owning an equal share of
+// the tiles' k-stages, but at least kMinStages of them; 0 when the workspace
+// cannot hold two accumulator images per workgroup or the counters (then the
+// launch does not use stream-K). *grid receives the workgroup count.
+inline int choose_streamk(int tiles, int nk, int cus, int tile_bytes, const void* wsp, int64_t ws_bytes, int* grid) {
+  constexpr int kMinStages = 8;
+  if (wsp == nullptr || cus <= 0 || tiles <= 0 || nk <= 0 || tiles > kSplitMaxTiles) return 0;
+  const int64_t total = (int64_t)tiles * nk;
+  int64_t g = min((int64_t)cus, total / kMinStages);
+  if (g < 1) g = 1;
+  const int64_t len = (total + g - 1) / g;
+  g = (total + len - 1) / len;  // every workgroup's range is non-empty
+  if (kSplitCntBytes + 2 * g * (int64_t)tile_bytes > ws_bytes) return 0;
+  *grid = (int)g;
+  return (int)len;
+}
+
+// kSK: stream-K (one workgroup per CU, equal k-stage shares; falls back to an
+// unsplit launch when the workspace cannot hold two images per workgroup).
 template <typename T, bool kW8A8, bool kRaw, int BM, int BN, int WM, int WN, int S, int MF, int KS, bool kSplit,
-          bool kNtW = false, bool kGlu = false, bool kRot = false, bool kDmaOnly = false, bool kDq = false>
+          bool kNtW = false, bool kGlu = false, bool kRot = false, bool kDmaOnly = false, bool kDq = false,
+          bool kSK = false>
 hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const float* ws, const void* bias, void* y,
                       int M, int N, int K, int group, int m_major, int splits, void* wsp, int64_t ws_bytes,
                       hipStream_t stream) {
   using C = Cfg<kW8A8, BM, BN, WM, WN, S, MF, KS>;
+  if constexpr (kSK) {
+    int g = 0;
+    const int len = choose_streamk(((M + BM - 1) / BM) * ((N + BN - 1) / BN), K / KS, device_cus(), BM * BN * 4, wsp,
+                                   ws_bytes, &g);
+    if (len <= 0)
+      return launch_dma<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, false, kNtW, kGlu, kRot, kDmaOnly, kDq>(
+          x, a_s, qw, ws, bias, y, M, N, K, group, m_major, 1, nullptr, 0, stream);
+    auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, true, kNtW, kGlu, kRot, kDmaOnly, kDq, true>;
+    static bool sk_attr_set = false;
+    if (!sk_attr_set) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+      if (e != hipSuccess) return e;
+      sk_attr_set = true;
+    }
+    kern<<<dim3(g), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias), y,
+                                                                M, N, K, group, m_major, 1, static_cast<char*>(wsp),
+                                                                len);
+    return hipGetLastError();
+  }
   auto kern = gemm_dma_kernel<T, kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu, kRot, kDmaOnly, kDq>;
   static bool attr_set = false;  // idempotent; a benign race sets it twice
   if (!attr_set) {
@@ -811,7 +900,7 @@ hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const f
   if (resident > 0 && units > resident) grid = resident - resident % 8;  // keep whole XCD rounds
   kern<<<dim3(grid), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias),
                                                                  y, M, N, K, group, m_major, splits,
-                                                                 static_cast<char*>(wsp));
+                                                                 static_cast<char*>(wsp), 0);
   return hipGetLastError();
 }
 
