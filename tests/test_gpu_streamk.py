@@ -38,6 +38,18 @@ def streamk(monkeypatch):
     monkeypatch.setenv("TVQ_STREAMK", "1")
 
 
+# Short K with fewer stages per workgroup (TVQ_STREAMK_MIN): tiles of 8 or
+# 16 stages are shared by two to eight workgroups.
+SHORT_K_CASES = [((64, 6144, 1024), 2), ((24, 3072, 1024), 1), ((17, 4096, 1024), 3), ((64, 1024, 2048), 1)]
+
+
+@pytest.mark.parametrize("case", SHORT_K_CASES, ids=lambda c: "x".join(map(str, c[0])) + f"-min{c[1]}")
+def test_streamk_short_k(hiplib, streamk, monkeypatch, case):
+    shape, min_stages = case
+    monkeypatch.setenv("TVQ_STREAMK_MIN", str(min_stages))
+    test_streamk_matches_unsplit_and_oracle(hiplib, None, shape)
+
+
 @pytest.mark.parametrize("shape", STREAMK_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_streamk_matches_unsplit_and_oracle(hiplib, streamk, shape):
     from nanovllm.quantization import _hip

@@ -27,12 +27,12 @@ KSPLIT_MAX_TILES = KSPLIT_CNT_BYTES // 4
 MIN_STAGES = 8
 
 
-def choose_streamk(tiles, nk, cus, tile_bytes, ws_bytes):
+def choose_streamk(tiles, nk, cus, tile_bytes, ws_bytes, min_stages=MIN_STAGES):
     """gemm_dma_kernel.h choose_streamk: (range length, grid) or (0, 0)."""
     if cus <= 0 or tiles <= 0 or nk <= 0 or tiles > KSPLIT_MAX_TILES:
         return 0, 0
     total = tiles * nk
-    g = max(1, min(cus, total // MIN_STAGES))
+    g = max(1, min(cus, total // min_stages))
     length = -(-total // g)
     g = -(-total // length)
     if KSPLIT_CNT_BYTES + 2 * g * tile_bytes > ws_bytes:
@@ -105,17 +105,17 @@ DECODE_SHAPES = [(64, 24576, 4096), (64, 6144, 4096), (64, 4096, 4096), (64, 409
 WS_BYTES = (16 << 20) + (64 << 10)   # tvq_gemm_workspace_bytes()
 
 
-@pytest.mark.parametrize("w8a8", [False, True])
+@pytest.mark.parametrize("min_stages", [1, 2, 4, 8])
 @pytest.mark.parametrize("shape", DECODE_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_streamk_partition_decode_shapes(shape, w8a8):
+def test_streamk_partition_decode_shapes(shape, min_stages):
     m, n, k = shape
     bm, bn = (64, 128) if m > 32 else (32, 64)
     tiles = -(-m // bm) * -(-n // bn)
     nk = k // 128
-    length, grid = choose_streamk(tiles, nk, 256, bm * bn * 4, WS_BYTES)
+    length, grid = choose_streamk(tiles, nk, 256, bm * bn * 4, WS_BYTES, min_stages)
     assert length > 0, "the default workspace holds two images per workgroup"
     assert grid <= 256
-    assert length >= MIN_STAGES or grid == 1
+    assert length >= min_stages or grid == 1
     check_partition(tiles, nk, length, grid)
 
 

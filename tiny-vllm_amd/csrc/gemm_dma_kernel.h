@@ -80,6 +80,8 @@
 // floor of the tiling, against which the full kernel is judged.
 #pragma once
 
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "tvq_common.h"
@@ -835,11 +837,18 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
 
 // Stream-K range length (tile-stages per workgroup) for `tiles` tiles of `nk`
 // k-stages on `cus` CUs: one workgroup per CU, each owning an equal share of
-// the tiles' k-stages, but at least kMinStages of them; 0 when the workspace
-// cannot hold two accumulator images per workgroup or the counters (then the
-// launch does not use stream-K). *grid receives the workgroup count.
+// the tiles' k-stages, but at least min_stages of them (TVQ_STREAMK_MIN,
+// default 8); 0 when the workspace cannot hold two accumulator images per
+// workgroup or the counters (then the launch does not use stream-K). *grid
+// receives the workgroup count.
+inline int streamk_min_stages() {
+  const char* env = getenv("TVQ_STREAMK_MIN");
+  const int v = env != nullptr ? atoi(env) : 0;
+  return v >= 1 && v <= 64 ? v : 8;
+}
+
 inline int choose_streamk(int tiles, int nk, int cus, int tile_bytes, const void* wsp, int64_t ws_bytes, int* grid) {
-  constexpr int kMinStages = 8;
+  const int kMinStages = streamk_min_stages();
   if (wsp == nullptr || cus <= 0 || tiles <= 0 || nk <= 0 || tiles > kSplitMaxTiles) return 0;
   const int64_t total = (int64_t)tiles * nk;
   int64_t g = min((int64_t)cus, total / kMinStages);
