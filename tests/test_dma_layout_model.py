@@ -30,6 +30,8 @@ CONFIGS = [
     (False, 64, 64, 2, 2, 32, 128),
     (False, 32, 64, 2, 2, 16, 128),
     (False, 64, 128, 2, 4, 16, 128),
+    (True, 256, 256, 2, 2, 32, 64),     # 4-wave prefill tiles (TVQ_PREFILL_W4=1)
+    (False, 128, 256, 2, 2, 32, 64),
 ]
 
 

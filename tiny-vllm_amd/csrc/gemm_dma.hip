@@ -39,7 +39,8 @@ namespace {
 using dma::launch_dma;
 
 enum class DmaCfg {
-  kI8_256x256, kI8_256x128, kI8_64x64, kI8_64x128, kI8_32x64, kH_128x256, kH_64x128, kH_64x64, kH_32x64, kH_64x128w8
+  kI8_256x256, kI8_256x128, kI8_64x64, kI8_64x128, kI8_32x64, kH_128x256, kH_64x128, kH_64x64, kH_32x64, kH_64x128w8,
+  kI8_256x256w4, kH_128x256w4
 };
 
 // Tile BM x BN, waves WM x WN, ring depth S, MFMA tile MF, per DmaCfg.
@@ -71,9 +72,15 @@ constexpr CfgInfo kInfo[] = {
      "dma_mfma_f16x_32x64_streamk"},
     {false, 64, 128, 2, 4, 4, 16, 128, "dma_mfma_f16x_64x128w8", "dma_mfma_f16x_64x128w8_splitk",
      "dma_mfma_f16x_64x128w8_streamk"},
+    // Prefill tiles of 4 waves with 4x4 fragments of 32x32 each (TVQ_PREFILL_W4=1): fewer LDS fragment
+    // reads per MFMA (8 per 16 instead of 6 per 8), one wave per SIMD, 64-k stages
+    {true, 256, 256, 2, 2, 4, 32, 64, "dma_mfma_i8_256x256w4", "dma_mfma_i8_256x256w4_splitk",
+     "dma_mfma_i8_256x256w4_streamk"},
+    {false, 128, 256, 2, 2, 4, 32, 64, "dma_mfma_f16x_128x256w4", "dma_mfma_f16x_128x256w4_splitk",
+     "dma_mfma_f16x_128x256w4_streamk"},
 };
 
-static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_64x128w8 + 1, "one entry per DmaCfg");
+static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_128x256w4 + 1, "one entry per DmaCfg");
 static_assert(kInfo[(int)DmaCfg::kI8_32x64].bm == 32 && kInfo[(int)DmaCfg::kH_128x256].bn == 256 &&
                   !kInfo[(int)DmaCfg::kH_64x64].w8a8 && kInfo[(int)DmaCfg::kI8_64x128].bn == 128,
               "kInfo follows the DmaCfg order");
@@ -105,6 +112,13 @@ bool streamk_shape(int64_t M) {
   return M <= 64 && env != nullptr && env[0] == '1';
 }
 
+// TVQ_PREFILL_W4=1 (read per call): the 4-wave prefill tiles in place of the
+// 8-wave 256x256 (W8A8) and 128x256 (W8A16) ones.
+bool prefill_w4() {
+  const char* env = getenv("TVQ_PREFILL_W4");
+  return env != nullptr && env[0] == '1';
+}
+
 DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
   if (streamk_shape(M)) {
     // the widest decode tiles: activation traffic per weight byte 2M/BN (W8A16), M/BN (W8A8)
@@ -113,7 +127,7 @@ DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
   }
   const bool split = split_shape(M, N, K);
   if (w8a8) {
-    if (tiles(M, N, 256, 256) >= 256) return DmaCfg::kI8_256x256;
+    if (tiles(M, N, 256, 256) >= 256) return prefill_w4() ? DmaCfg::kI8_256x256w4 : DmaCfg::kI8_256x256;
     if (tiles(M, N, 256, 128) >= 200) return DmaCfg::kI8_256x128;
     if (M > 256 || (split && M > 32)) return DmaCfg::kI8_64x64;
     if (M > 32 && M <= 64 && N >= 16384) return DmaCfg::kI8_64x128;
@@ -123,7 +137,7 @@ DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
     if (M > 64 && tiles(M, N, 64, 64) >= 256) return DmaCfg::kI8_64x64;
     return DmaCfg::kI8_32x64;
   }
-  if (tiles(M, N, 128, 256) >= 200) return DmaCfg::kH_128x256;
+  if (tiles(M, N, 128, 256) >= 200) return prefill_w4() ? DmaCfg::kH_128x256w4 : DmaCfg::kH_128x256;
   if (M > 256) return DmaCfg::kH_64x128;
   if (M <= 64) {
     if (split && M > 32) return DmaCfg::kH_64x64;
@@ -172,6 +186,7 @@ int splits_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64_
   case DmaCfg::C: return splits_of<DmaCfg::C>(M, N, K, ws, ws_bytes);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4)
 #undef TVQ_CASE
   }
   return 1;
@@ -183,6 +198,7 @@ int streamk_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64
   case DmaCfg::C: return streamk_len<DmaCfg::C>(M, N, K, ws, ws_bytes);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4)
 #undef TVQ_CASE
   }
   return 0;
@@ -223,6 +239,7 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
   if constexpr (kW8A8) {
     switch (choose(true, a.M, a.N, a.K)) {
       case DmaCfg::kI8_256x256: return go<T, kRaw, DmaCfg::kI8_256x256>(a, s);
+      case DmaCfg::kI8_256x256w4: return go<T, kRaw, DmaCfg::kI8_256x256w4>(a, s);
       case DmaCfg::kI8_256x128: return go<T, kRaw, DmaCfg::kI8_256x128>(a, s);
       case DmaCfg::kI8_64x64: return go<T, kRaw, DmaCfg::kI8_64x64>(a, s);
       case DmaCfg::kI8_64x128: return go<T, kRaw, DmaCfg::kI8_64x128>(a, s);
@@ -231,6 +248,7 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
   } else {
     switch (choose(false, a.M, a.N, a.K)) {
       case DmaCfg::kH_128x256: return go<T, false, DmaCfg::kH_128x256>(a, s);
+      case DmaCfg::kH_128x256w4: return go<T, false, DmaCfg::kH_128x256w4>(a, s);
       case DmaCfg::kH_64x128: return go<T, false, DmaCfg::kH_64x128>(a, s);
       case DmaCfg::kH_32x64: return go<T, false, DmaCfg::kH_32x64>(a, s);
       case DmaCfg::kH_64x128w8: return go<T, false, DmaCfg::kH_64x128w8>(a, s);
@@ -303,6 +321,7 @@ template <typename T>
 hipError_t dq_t(const GemmArgs& a, hipStream_t s) {
   switch (choose(false, a.M, a.N, a.K)) {
     case DmaCfg::kH_128x256: return dq_of<T, DmaCfg::kH_128x256>(a, s);
+    case DmaCfg::kH_128x256w4: return dq_of<T, DmaCfg::kH_128x256w4>(a, s);
     case DmaCfg::kH_64x128: return dq_of<T, DmaCfg::kH_64x128>(a, s);
     case DmaCfg::kH_32x64: return dq_of<T, DmaCfg::kH_32x64>(a, s);
     case DmaCfg::kH_64x128w8: return dq_of<T, DmaCfg::kH_64x128w8>(a, s);
@@ -320,6 +339,7 @@ hipError_t launch_dma_floor(const GemmArgs& a, hipStream_t stream) {
   case DmaCfg::C: return floor_of<DmaCfg::C>(a, stream);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4)
 #undef TVQ_CASE
   }
   return hipErrorInvalidValue;
