@@ -128,6 +128,27 @@ def test_select_path_buckets(hiplib):
         sp(9, 1, 1, 1)
 
 
+def test_select_path_opt_in_switches(hiplib, monkeypatch):
+    """TVQ_PREFILL_W4 swaps the 8-wave prefill tiles for the 4-wave ones;
+    TVQ_STREAMK moves decode-size DMA shapes onto the widest decode tiles
+    (the "_streamk" suffix needs a device: it depends on the CU count)."""
+    from nanovllm.quantization import _hip
+    sp = _hip.select_path
+    monkeypatch.setenv("TVQ_PREFILL_W4", "1")
+    assert sp(_hip.OP_W8A8, 8192, 6144, 1024) == "dma_mfma_i8_256x256w4"
+    assert sp(_hip.OP_W8A16, 8192, 1024, 3072) == "dma_mfma_f16x_128x256w4"
+    assert sp(_hip.OP_W8A8, 8192, 1024, 3072) == "dma_mfma_i8_256x128"     # fewer than 256 such tiles
+    assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_64x64"        # decode sizes unchanged
+    monkeypatch.delenv("TVQ_PREFILL_W4")
+    monkeypatch.setenv("TVQ_STREAMK", "1")
+    assert sp(_hip.OP_W8A16, 64, 4096, 12288) == "dma_mfma_f16x_64x128w8"   # instead of split-K 64x64
+    assert sp(_hip.OP_W8A8, 48, 4096, 4096) == "dma_mfma_i8_64x128"
+    assert sp(_hip.OP_W8A16, 32, 4096, 4096) == "dma_mfma_f16x_32x64"
+    assert sp(_hip.OP_W8A8, 16, 24576, 4096) == "dma_mfma_i8_32x64"
+    assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_64x64"        # M > 64 unchanged
+    assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "gemv_dot2_f16x"            # other families unchanged
+
+
 # ------------------------------------------------------------------ Python API
 
 class _Layer(torch.nn.Module):
