@@ -54,7 +54,9 @@
 // slots 0..S-2 and only then runs the epilogue, so the operand fetch of tile
 // i+1 overlaps the output stores of tile i. The epilogue needs no global
 // loads (which would queue behind that DMA): the tile's per-token scales,
-// per-channel scales and bias are fetched at tile start and parked in LDS.
+// per-channel scales and bias are loaded into registers at tile start and
+// parked in LDS after the tile's last k-stage (where the wait for them is
+// free; at tile start it would drain the ring).
 // It stages each wave's MF-row slice of its output through a wave-private
 // area of the idle ring slot S-1 and writes whole row segments of 16-byte
 // stores.
@@ -382,20 +384,26 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   static_assert(kSub % 2 == 0, "fragment buffers alternate per sub-step across stages");
 
   // ---- per-tile scales and bias, parked in LDS for the epilogue ----------
+  // The values are loaded into registers with the tile's first stage DMAs
+  // (as raw bits; the bias is converted only when stored) and written to LDS
+  // after the tile's last k-stage, where every DMA op of the tile has
+  // already been waited for: the compiler's wait for the loads (vmcnt(0): it
+  // cannot count the ops in flight across the persistent loop) then costs
+  // nothing. Written at tile start, that wait drained the whole ring there.
   float* sc = reinterpret_cast<float*>(smem + C::kRingBytes);  // [a_s: BM | w_s: BN | bias: BN]
   constexpr int kScPer = (C::kScN + C::kThreads - 1) / C::kThreads;
-  float scv[kScPer];
+  uint32_t scv[kScPer];
   auto load_scales = [&](int m0, int n0) {
 #pragma unroll
     for (int u = 0; u < kScPer; ++u) {
       const int idx = (int)threadIdx.x + u * C::kThreads;
-      float v = 0.0f;
+      uint32_t v = 0;
       if (idx < BM) {
-        if constexpr (kW8A8) v = a_scales[min(m0 + idx, M - 1)];
+        if constexpr (kW8A8) v = __builtin_bit_cast(uint32_t, a_scales[min(m0 + idx, M - 1)]);
       } else if (idx < BM + BN) {
-        v = ws[min(n0 + idx - BM, N - 1)];
+        v = __builtin_bit_cast(uint32_t, ws[min(n0 + idx - BM, N - 1)]);
       } else if (idx < C::kScN && bias != nullptr) {
-        v = to_float<T>(bias[min(n0 + idx - BM - BN, N - 1)]);
+        v = bias[min(n0 + idx - BM - BN, N - 1)];
       }
       scv[u] = v;
     }
@@ -404,7 +412,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
 #pragma unroll
     for (int u = 0; u < kScPer; ++u) {
       const int idx = (int)threadIdx.x + u * C::kThreads;
-      if (idx < C::kScN) sc[idx] = scv[u];
+      if (idx < BM + BN)
+        sc[idx] = __builtin_bit_cast(float, scv[u]);
+      else if (idx < C::kScN)
+        sc[idx] = to_float<T>((uint16_t)scv[u]);
     }
   };
 
@@ -468,8 +479,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     wait_stage<C::kLPW, S>(min(S - 2, cur_nk - 1));
     barrier();
     TVQ_TL_MARK(1);
-    // after the barrier: the previous tile's epilogue no longer reads them
-    if constexpr (!kRaw && !kDmaOnly) store_scales();
     if (S - 1 < cur_nk) issue(S - 1);
     if constexpr (!kDmaOnly) load_frags(0, 0, 0);
 
@@ -552,8 +561,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       }
     }
 
-    // Every wave has consumed its last fragments: the ring is free.
+    // Every wave has consumed its last fragments: the ring is free. The
+    // previous tile's epilogue finished before this tile's first barrier, so
+    // the scale area is free too: park this tile's scales there (their loads
+    // completed with the tile's DMA) and publish them before the epilogue.
     barrier();
+    if constexpr (!kRaw && !kDmaOnly) {
+      store_scales();
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      barrier();
+    }
     TVQ_TL_MARK(2);
     // ---- next tile: start its operand stream before this tile's stores ----
     bool more;
