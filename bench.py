@@ -222,7 +222,7 @@ def sweep_cases():
     return cases
 
 
-def run_sweep(lib, dev, quick=False):
+def run_sweep(lib, dev, quick=False, tag=""):
     from nanovllm.quantization import _hip
     L = Launcher(lib, dev)
     out = []
@@ -231,7 +231,7 @@ def run_sweep(lib, dev, quick=False):
         cases = [c for c in cases if c[0] in ("cfg1", "cfg2") or (c[0].startswith("cfg3") and c[1] == "w8a8")]
     # full records go to a file (the JSON line carries a compact form)
     (ROOT / "gpurun_out").mkdir(exist_ok=True)
-    log = open(ROOT / "gpurun_out" / "bench_sweep.jsonl", "w")
+    log = open(ROOT / "gpurun_out" / (f"bench_sweep_{tag}.jsonl" if tag else "bench_sweep.jsonl"), "w")
     for ci, (tag, mode, m, n, k) in enumerate(cases):
         if ci % 16 == 0:
             print(f"sweep case {ci}/{len(cases)}", file=sys.stderr, flush=True)
@@ -411,6 +411,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 engine leg")
+    ap.add_argument("--tag", default="", help="suffix of the sweep record file (gpurun_out/bench_sweep_TAG.jsonl), "
+                                              "for runs under other kernel switches")
     ap.add_argument("--profile", action="store_true",
                     help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
@@ -501,7 +503,7 @@ def main():
     del x, qs, ss
     torch.cuda.empty_cache()
 
-    sweep = None if args.no_sweep else run_sweep(lib, dev, quick=args.quick)
+    sweep = None if args.no_sweep else run_sweep(lib, dev, quick=args.quick, tag=args.tag)
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
