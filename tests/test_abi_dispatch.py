@@ -146,7 +146,11 @@ def test_select_path_opt_in_switches(hiplib, monkeypatch):
     assert sp(_hip.OP_W8A16, 32, 4096, 4096) == "dma_mfma_f16x_32x64"
     assert sp(_hip.OP_W8A8, 16, 24576, 4096) == "dma_mfma_i8_32x64"
     assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_64x64"        # M > 64 unchanged
-    assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "gemv_dot2_f16x"            # other families unchanged
+    assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "gemv_dot2_f16x"            # the GEMV keeps M <= 2
+    assert sp(_hip.OP_W8A16, 16, 4096, 1024) == "dma_mfma_f16x_16x128"     # M <= 16: 16-row tiles
+    assert sp(_hip.OP_W8A16, 3, 24576, 4096) == "dma_mfma_f16x_16x128"
+    assert sp(_hip.OP_W8A8, 8, 24576, 4096) == "dma_mfma_i8_32x64"
+    assert sp(_hip.OP_W8A8, 8, 4096, 1040) == "skinny_mfma_i8_m16"        # K % 128 != 0 keeps skinny
 
 
 # ------------------------------------------------------------------ Python API

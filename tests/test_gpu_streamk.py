@@ -26,7 +26,8 @@ pytestmark = [pytest.mark.gpu,
 # Decode shapes: 8B gate_up / qkv / o / down at M = 64 and 48, Qwen3-0.6B
 # shapes (config 1 among them), ragged M and N, and K with few stages.
 STREAMK_SHAPES = [(64, 24576, 4096), (64, 6144, 4096), (48, 4096, 4096), (64, 4096, 12288), (64, 6144, 1024),
-                  (40, 1000, 2048), (33, 136, 2048), (24, 3072, 1024), (17, 4096, 1024), (64, 2048, 128)]
+                  (40, 1000, 2048), (33, 136, 2048), (24, 3072, 1024), (17, 4096, 1024), (64, 2048, 128),
+                  (16, 24576, 4096), (8, 4096, 12288), (3, 6144, 4096), (13, 1000, 2048)]
 
 
 def _log_case(**kw):

@@ -101,15 +101,24 @@ def check_partition(tiles, nk, length, grid):
 # (M, N, K) decode shapes x the tiles the dispatcher uses for them with stream-K
 DECODE_SHAPES = [(64, 24576, 4096), (64, 6144, 4096), (64, 4096, 4096), (64, 4096, 12288), (48, 6144, 4096),
                  (64, 6144, 1024), (64, 4096, 1024), (64, 3072, 1024), (64, 1024, 3072), (64, 1024, 2048),
-                 (32, 24576, 4096), (24, 4096, 4096), (17, 1000, 2048), (33, 136, 2048), (20, 4096, 12288)]
+                 (32, 24576, 4096), (24, 4096, 4096), (17, 1000, 2048), (33, 136, 2048), (20, 4096, 12288),
+                 (16, 24576, 4096), (8, 4096, 12288), (3, 6144, 4096), (13, 1000, 2048)]
 WS_BYTES = (16 << 20) + (64 << 10)   # tvq_gemm_workspace_bytes()
 
 
+def streamk_tile(w8a8, m):
+    """gemm_dma.hip choose() under TVQ_STREAMK=1."""
+    if m > 32:
+        return 64, 128
+    return (32, 64) if (w8a8 or m > 16) else (16, 128)
+
+
+@pytest.mark.parametrize("w8a8", [False, True])
 @pytest.mark.parametrize("min_stages", [1, 2, 4, 8])
 @pytest.mark.parametrize("shape", DECODE_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_streamk_partition_decode_shapes(shape, min_stages):
+def test_streamk_partition_decode_shapes(shape, min_stages, w8a8):
     m, n, k = shape
-    bm, bn = (64, 128) if m > 32 else (32, 64)
+    bm, bn = streamk_tile(w8a8, m)
     tiles = -(-m // bm) * -(-n // bn)
     nk = k // 128
     length, grid = choose_streamk(tiles, nk, 256, bm * bn * 4, WS_BYTES, min_stages)

@@ -110,6 +110,7 @@ Path select_gemm_path(const GemmArgs& a) {
   Path forced;
   if (forced_path(a, &forced)) return forced;
   if (gemv_shape_ok(a.M, a.K)) return Path::kGemv;
+  if (a.M > kGemvMaxM && dma_shape_ok(a.K) && dma_streamk_on(a.M)) return Path::kDma;
   if (a.M <= kSkinnyMaxM) {
     if (dma_shape_ok(a.K) && (a.M > kDmaMinM || (a.M > 8 && a.N * a.K >= kDmaMidWeights))) return Path::kDma;
     return stream_shape_ok(a.M, a.N, a.K) ? Path::kStream : Path::kSkinny;
@@ -120,6 +121,7 @@ Path select_gemm_path(const GemmArgs& a) {
 const char* gemm_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, bool aligned) {
   if (!aligned || !shape_vec_ok(K)) return "generic_simt";
   if (gemv_shape_ok(M, K)) return w8a8 ? "gemv_dot4_i8" : "gemv_dot2_f16x";
+  if (M > kGemvMaxM && dma_shape_ok(K) && dma_streamk_on(M)) return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
   if (M <= kSkinnyMaxM && dma_shape_ok(K) && (M > kDmaMinM || (M > 8 && N * K >= kDmaMidWeights)))
     return dma_path_name(w8a8, M, N, K, kGemmWorkspaceBytes);
   if (M <= kSkinnyMaxM && stream_shape_ok(M, N, K)) {

@@ -40,7 +40,7 @@ using dma::launch_dma;
 
 enum class DmaCfg {
   kI8_256x256, kI8_256x128, kI8_64x64, kI8_64x128, kI8_32x64, kH_128x256, kH_64x128, kH_64x64, kH_32x64, kH_64x128w8,
-  kI8_256x256w4, kH_128x256w4
+  kI8_256x256w4, kH_128x256w4, kH_16x128
 };
 
 // Tile BM x BN, waves WM x WN, ring depth S, MFMA tile MF, per DmaCfg.
@@ -78,9 +78,13 @@ constexpr CfgInfo kInfo[] = {
      "dma_mfma_i8_256x256w4_streamk"},
     {false, 128, 256, 2, 2, 4, 32, 64, "dma_mfma_f16x_128x256w4", "dma_mfma_f16x_128x256w4_splitk",
      "dma_mfma_f16x_128x256w4_streamk"},
+    // W8A16 at M <= 16 under stream-K: one 16-token row of MFMA blocks, so the
+    // activation panel is a quarter of the weight bytes (2 * 16 / 128)
+    {false, 16, 128, 1, 4, 4, 16, 128, "dma_mfma_f16x_16x128", "dma_mfma_f16x_16x128_splitk",
+     "dma_mfma_f16x_16x128_streamk"},
 };
 
-static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_128x256w4 + 1, "one entry per DmaCfg");
+static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_16x128 + 1, "one entry per DmaCfg");
 static_assert(kInfo[(int)DmaCfg::kI8_32x64].bm == 32 && kInfo[(int)DmaCfg::kH_128x256].bn == 256 &&
                   !kInfo[(int)DmaCfg::kH_64x64].w8a8 && kInfo[(int)DmaCfg::kI8_64x128].bn == 128,
               "kInfo follows the DmaCfg order");
@@ -123,7 +127,7 @@ DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
   if (streamk_shape(M)) {
     // the widest decode tiles: activation traffic per weight byte 2M/BN (W8A16), M/BN (W8A8)
     if (w8a8) return M > 32 ? DmaCfg::kI8_64x128 : DmaCfg::kI8_32x64;
-    return M > 32 ? DmaCfg::kH_64x128w8 : DmaCfg::kH_32x64;
+    return M > 32 ? DmaCfg::kH_64x128w8 : (M > 16 ? DmaCfg::kH_32x64 : DmaCfg::kH_16x128);
   }
   const bool split = split_shape(M, N, K);
   if (w8a8) {
@@ -186,7 +190,7 @@ int splits_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64_
   case DmaCfg::C: return splits_of<DmaCfg::C>(M, N, K, ws, ws_bytes);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
-    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128)
 #undef TVQ_CASE
   }
   return 1;
@@ -198,7 +202,7 @@ int streamk_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64
   case DmaCfg::C: return streamk_len<DmaCfg::C>(M, N, K, ws, ws_bytes);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
-    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128)
 #undef TVQ_CASE
   }
   return 0;
@@ -249,6 +253,7 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
     switch (choose(false, a.M, a.N, a.K)) {
       case DmaCfg::kH_128x256: return go<T, false, DmaCfg::kH_128x256>(a, s);
       case DmaCfg::kH_128x256w4: return go<T, false, DmaCfg::kH_128x256w4>(a, s);
+      case DmaCfg::kH_16x128: return go<T, false, DmaCfg::kH_16x128>(a, s);
       case DmaCfg::kH_64x128: return go<T, false, DmaCfg::kH_64x128>(a, s);
       case DmaCfg::kH_32x64: return go<T, false, DmaCfg::kH_32x64>(a, s);
       case DmaCfg::kH_64x128w8: return go<T, false, DmaCfg::kH_64x128w8>(a, s);
@@ -258,6 +263,8 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+bool dma_streamk_on(int64_t M) { return streamk_shape(M); }
 
 // K % 128 == 0 (whole stages), and K <= 2^22 so that every per-lane DMA
 // source offset (tile row x row bytes + stage offset, at most 256 x 2K bytes)
@@ -322,6 +329,7 @@ hipError_t dq_t(const GemmArgs& a, hipStream_t s) {
   switch (choose(false, a.M, a.N, a.K)) {
     case DmaCfg::kH_128x256: return dq_of<T, DmaCfg::kH_128x256>(a, s);
     case DmaCfg::kH_128x256w4: return dq_of<T, DmaCfg::kH_128x256w4>(a, s);
+    case DmaCfg::kH_16x128: return dq_of<T, DmaCfg::kH_16x128>(a, s);
     case DmaCfg::kH_64x128: return dq_of<T, DmaCfg::kH_64x128>(a, s);
     case DmaCfg::kH_32x64: return dq_of<T, DmaCfg::kH_32x64>(a, s);
     case DmaCfg::kH_64x128w8: return dq_of<T, DmaCfg::kH_64x128w8>(a, s);
@@ -339,7 +347,7 @@ hipError_t launch_dma_floor(const GemmArgs& a, hipStream_t stream) {
   case DmaCfg::C: return floor_of<DmaCfg::C>(a, stream);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
-    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128)
 #undef TVQ_CASE
   }
   return hipErrorInvalidValue;

@@ -71,6 +71,9 @@ hipError_t launch_dma_floor(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_dma_dq(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_generic_dq(const GemmArgs& a, hipStream_t stream);
 bool dma_shape_ok(int64_t K);
+// TVQ_STREAMK=1 and M <= 64: decode-size DMA launches use stream-K, and the
+// dispatcher sends every such M above the GEMV range (M > 2) to the DMA tiles.
+bool dma_streamk_on(int64_t M);
 // Path name, with a "_splitk" suffix when a workspace of the given size makes
 // the launch split K (which needs the device: without one it never splits).
 const char* dma_path_name(bool w8a8, int64_t M, int64_t N, int64_t K, int64_t workspace_bytes);
