@@ -390,22 +390,31 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
   // already been waited for: the compiler's wait for the loads (vmcnt(0): it
   // cannot count the ops in flight across the persistent loop) then costs
   // nothing. Written at tile start, that wait drained the whole ring there.
+  // Every lane issues the same loads (addresses selected and clamped, no
+  // per-lane branch): a load register that another branch writes makes the
+  // compiler wait vmcnt(0) on it, which would drain the ring right after the
+  // tile's stage DMAs. The bias goes to its own registers under a
+  // wave-uniform branch.
   float* sc = reinterpret_cast<float*>(smem + C::kRingBytes);  // [a_s: BM | w_s: BN | bias: BN]
   constexpr int kScPer = (C::kScN + C::kThreads - 1) / C::kThreads;
-  uint32_t scv[kScPer];
+  float scv[kScPer];
+  uint16_t sbv[kScPer];
   auto load_scales = [&](int m0, int n0) {
 #pragma unroll
     for (int u = 0; u < kScPer; ++u) {
       const int idx = (int)threadIdx.x + u * C::kThreads;
-      uint32_t v = 0;
-      if (idx < BM) {
-        if constexpr (kW8A8) v = __builtin_bit_cast(uint32_t, a_scales[min(m0 + idx, M - 1)]);
-      } else if (idx < BM + BN) {
-        v = __builtin_bit_cast(uint32_t, ws[min(n0 + idx - BM, N - 1)]);
-      } else if (idx < C::kScN && bias != nullptr) {
-        v = bias[min(n0 + idx - BM - BN, N - 1)];
+      // idx < BM: the token's scale (W8A8); otherwise channel idx - BM (the
+      // slots past BM + BN load a valid channel and are not used)
+      const float* p = ws + min(n0 + max(idx - BM, 0), N - 1);
+      if constexpr (kW8A8) p = idx < BM ? a_scales + min(m0 + idx, M - 1) : p;
+      scv[u] = *p;
+    }
+    if (bias != nullptr) {
+#pragma unroll
+      for (int u = 0; u < kScPer; ++u) {
+        const int idx = (int)threadIdx.x + u * C::kThreads;
+        sbv[u] = bias[min(n0 + max(idx - BM - BN, 0), N - 1)];
       }
-      scv[u] = v;
     }
   };
   auto store_scales = [&]() {
@@ -413,9 +422,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
     for (int u = 0; u < kScPer; ++u) {
       const int idx = (int)threadIdx.x + u * C::kThreads;
       if (idx < BM + BN)
-        sc[idx] = __builtin_bit_cast(float, scv[u]);
+        sc[idx] = scv[u];
       else if (idx < C::kScN)
-        sc[idx] = to_float<T>((uint16_t)scv[u]);
+        sc[idx] = bias != nullptr ? to_float<T>(sbv[u]) : 0.0f;
     }
   };
 
