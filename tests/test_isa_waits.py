@@ -122,3 +122,38 @@ def test_mfma_loop_has_no_spills_or_extra_vmem_waits(assembly, cfg):
         if "vmcnt" in l and l.startswith("s_waitcnt"):
             ahead = [x for x in span[i + 1:i + 40] if not x.startswith(".")][:16]
             assert any(x.startswith("s_barrier") for x in ahead), f"vmcnt wait not at a stage crossing: {l}"
+
+
+@pytest.fixture(scope="module")
+def skinny_assembly(tmp_path_factory):
+    hipcc = _hipcc()
+    if hipcc is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa_skinny") / "skinny.s"
+    src = ROOT / "tiny-vllm_amd" / "csrc" / "gemm_skinny.hip"
+    cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    lines = out.read_text().split("\n")
+    starts = [i for i, l in enumerate(lines) if l.startswith("_ZN3tvq12_GLOBAL__N_113skinny_kernel") and ": " in l]
+    starts.append(len(lines))
+    return {lines[a].split(":")[0]: [l.strip() for l in lines[a:b] if l.strip() and not l.strip().startswith(";")]
+            for a, b in zip(starts, starts[1:])}
+
+
+def test_skinny_run_issues_all_loads_before_its_mfmas(skinny_assembly):
+    """Decode M <= 16 (one 16-token block, one 16-row block, 8 chunks per run):
+    the full run's 8 weight + 16 activation loads (W8A16) or 8 + 8 (W8A8) are
+    in flight before the first MFMA waits on any of them."""
+    checked = 0
+    for name, code in skinny_assembly.items():
+        m = re.search(r"skinny_kernelINS_\d(BF16|F16)ELb(\d)ELb0ELi1ELi1ELi(\d+)ELi8E", name)
+        if not m:
+            continue
+        w8a8 = m.group(2) == "1"
+        first = next(i for i, l in enumerate(code) if l.startswith("v_mfma"))
+        loads = sum(1 for l in code[:first] if l.startswith("global_load_dwordx4"))
+        assert loads >= (16 if w8a8 else 24), (name, loads)
+        checked += 1
+    assert checked >= 4

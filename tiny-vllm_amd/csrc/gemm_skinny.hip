@@ -103,6 +103,9 @@ __global__ __launch_bounds__(64 * kWaves) void skinny_kernel(const void* __restr
         }
       }
     }
+    // Every load of the run is issued before the first MFMA (left alone, the
+    // scheduler sinks them among the MFMAs and keeps only ~10 in flight).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
