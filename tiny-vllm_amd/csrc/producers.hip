@@ -130,13 +130,17 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t* __r
   // every load of the row is issued before the first use (clamped index, no
   // branch around the loads), so they are all in flight together
   const int vmax = nvec > 0 ? nvec - 1 : 0;
-  u32x4 xin[NI], rin[NI];
+  // The norm weights are loaded with them: issued after the row reduction,
+  // they added an L2 round trip to every row.
+  u32x4 xin[NI], rin[NI], win[NI];
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int v = min(it * TPR + t, vmax);
     xin[it] = ldg128_stream(xr + (int64_t)v * 8);
     if constexpr (kRes) rin[it] = ldg128_stream(res + row * K + (int64_t)v * 8);
+    win[it] = ldg128(w + (int64_t)v * 8);
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int v = it * TPR + t;
@@ -161,9 +165,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t* __r
   }
   ss = row_reduce<TPR, false>(ss, lds_ss);
   const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)K) + eps));
-  u32x4 yv[NI], win[NI];
-#pragma unroll
-  for (int it = 0; it < NI; ++it) win[it] = ldg128(w + (int64_t)min(it * TPR + t, vmax) * 8);
+  u32x4 yv[NI];
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const int v = it * TPR + t;
@@ -201,21 +203,28 @@ __global__ __launch_bounds__(kBlock) void silu_mul_vec_kernel(const uint16_t* __
     gin[it] = ldg128_stream(g + (int64_t)v * 8);
     uin[it] = ldg128_stream(u + (int64_t)v * 8);
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
+  // Every lane computes (its loads were clamped into the row), then the
+  // stores follow, guarded. Computing inside the guarded stores let the
+  // compiler sink the last loads past the first stores.
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
-    const int v = it * TPR + t;
-    if (v < nvec) {
-      const u32x4 gv = gin[it];
-      const u32x4 uv = uin[it];
-      float o[8];
+    const u32x4 gv = gin[it];
+    const u32x4 uv = uin[it];
+    float o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float a = elt<T>(gv, i);
-        o[i] = silu_f(a) * elt<T>(uv, i);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float a = elt<T>(gv, i);
+      o[i] = silu_f(a) * elt<T>(uv, i);
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) yv[it][i] = pack2<T>(o[2 * i], o[2 * i + 1]);
-      if constexpr (kY) *reinterpret_cast<u32x4*>(y + row * I + (int64_t)v * 8) = yv[it];
+    for (int i = 0; i < 4; ++i) yv[it][i] = pack2<T>(o[2 * i], o[2 * i + 1]);
+  }
+  if constexpr (kY) {
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int v = it * TPR + t;
+      if (v < nvec) *reinterpret_cast<u32x4*>(y + row * I + (int64_t)v * 8) = yv[it];
     }
   }
   if constexpr (kQ) quant_store<T, TPR, NI>(yv, nvec, t, rl.live, 1e-8f, xq + row * I, a_scales + row, lds_max);
