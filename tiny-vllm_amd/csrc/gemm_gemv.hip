@@ -45,13 +45,39 @@ __device__ __forceinline__ float dot2<F16>(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
 }
 
-__device__ __forceinline__ float lane_sum(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+// Sum of NV per-lane values over the 64 lanes of a wave, all NV at once: at
+// each of the first log2(NV) steps (lane offsets 32, 16, ...) a lane keeps
+// the half of its values selected by its lane bit, sends the other half to
+// its partner across that bit and adds the partner's copy of the kept half,
+// so the values in flight halve every step (NV - 1 exchanges instead of
+// 6 * NV). The remaining offsets then sum within each group. Afterwards every
+// lane of group j = lane / (64 / NV) holds the total of value j. The order of
+// the additions is fixed, so the result is deterministic.
+// One halving step over the first N values at lane offset OFF, then the
+// next; every index is a compile-time constant (the values stay in VGPRs).
+template <int N, int OFF, int NV, typename Acc>
+__device__ __forceinline__ Acc fold_step(Acc (&c)[NV], int lane) {
+  if constexpr (N > 1) {
+    const bool hi = (lane & OFF) != 0;   // keep the upper half
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const Acc send = hi ? c[i] : c[i + N / 2];
+      const Acc keep = hi ? c[i + N / 2] : c[i];
+      c[i] = keep + __shfl_xor(send, OFF, kWave);
+    }
+    return fold_step<N / 2, OFF / 2>(c, lane);
+  } else {
+    Acc v = c[0];
+#pragma unroll
+    for (int off = OFF; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+  }
 }
-__device__ __forceinline__ int32_t lane_sum(int32_t v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+
+template <int NV, typename Acc>
+__device__ __forceinline__ Acc fold_sum(Acc (&c)[NV]) {
+  static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "a power of two up to 64 values");
+  return fold_step<NV, 32>(c, (int)__lane_id());
 }
 
 template <typename T, bool kW8A8, bool kRaw, int MM, int R, int WPG, int CPW>
@@ -129,41 +155,70 @@ __global__ __launch_bounds__(256) void gemv_kernel(const void* __restrict__ xv, 
   }
 
   // ---- reduction: 64 lanes, then the WPG waves of the group ------------------
-#pragma unroll
-  for (int m = 0; m < MM; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = lane_sum(acc[m][r]);
-
-  constexpr int kOut = MM * R;               // outputs per group
+  constexpr int kOut = MM * R;               // outputs per group, value j = m * R + r
   static_assert(kOut <= 64, "one lane per output");
   __shared__ Acc red[4][kOut];
-  if constexpr (WPG > 1) {
-    if (lane == 0) {
+  Acc v;
+  if constexpr (CPW < 3) {
+    constexpr int kGroup = 64 / kOut;        // lanes per value after fold_sum
+    Acc flat[kOut];
 #pragma unroll
-      for (int m = 0; m < MM; ++m)
+    for (int m = 0; m < MM; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r) red[wave][m * R + r] = acc[m][r];
+      for (int r = 0; r < R; ++r) flat[m * R + r] = acc[m][r];
+    const Acc total = fold_sum<kOut>(flat);  // total of value lane / kGroup
+    if constexpr (WPG > 1) {
+      if (lane % kGroup == 0) red[wave][lane / kGroup] = total;
+      __syncthreads();
+      if (wig != 0) return;
     }
-    __syncthreads();
-    if (wig != 0) return;
+    // one wave per group: lane j takes value j from the first lane of group j
+    // (before any lane leaves: the source lanes may lie past kOut)
+    Acc own{};
+    if constexpr (WPG == 1) own = __shfl(total, (lane % kOut) * kGroup, kWave);
+    if (lane >= kOut) return;
+    if constexpr (WPG > 1) {
+      v = red[grp * WPG][lane];
+#pragma unroll
+      for (int w = 1; w < WPG; ++w) v += red[grp * WPG + w][lane];
+    } else {
+      v = own;
+    }
+  } else {
+    // three chunks per wave: one butterfly per value, reduced in place (the
+    // fold's extra registers would cost a wave per SIMD: 128 -> 159 VGPRs)
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc[m][r] += __shfl_xor(acc[m][r], off, kWave);
+    if constexpr (WPG > 1) {
+      if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) red[wave][m * R + r] = acc[m][r];
+      }
+      __syncthreads();
+      if (wig != 0) return;
+    }
+    if (lane >= kOut) return;
+    if constexpr (WPG > 1) {
+      v = red[grp * WPG][lane];
+#pragma unroll
+      for (int w = 1; w < WPG; ++w) v += red[grp * WPG + w][lane];
+    } else {
+      v = acc[0][0];   // every lane holds every sum; pick this lane's one
+#pragma unroll
+      for (int mm = 0; mm < MM; ++mm)
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr)
+          if (mm * R + rr == lane) v = acc[mm][rr];
+    }
   }
-  if (lane >= kOut) return;
   const int m = lane / R;
   const int r = lane % R;
-  Acc v;
-  if constexpr (WPG > 1) {
-    v = red[grp * WPG][lane];
-#pragma unroll
-    for (int w = 1; w < WPG; ++w) v += red[grp * WPG + w][lane];
-  } else {
-    // every lane holds every sum after the butterfly; pick this lane's one
-    v = acc[0][0];
-#pragma unroll
-    for (int mm = 0; mm < MM; ++mm)
-#pragma unroll
-      for (int rr = 0; rr < R; ++rr)
-        if (mm * R + rr == lane) v = acc[mm][rr];
-  }
   const int n = row0 + r;
   if (m >= M || n >= N) return;
   if constexpr (kRaw) {
