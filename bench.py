@@ -411,8 +411,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 engine leg")
-    ap.add_argument("--tag", default="", help="suffix of the sweep record file (gpurun_out/bench_sweep_TAG.jsonl), "
-                                              "for runs under other kernel switches")
+    ap.add_argument("--tag", default="", help="suffix of the sweep record file (bench_sweep_TAG.jsonl in the output "
+                                              "folder), for runs under other kernel switches")
     ap.add_argument("--profile", action="store_true",
                     help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
