@@ -95,18 +95,26 @@ def roofline_for(mode, m, n, k, seconds):
 # ---------------------------------------------------------------- inputs
 
 def make_inputs(mode, m, n, k, dev, seed=0, pool_bytes=POOL_BYTES, max_copies=256):
-    """Activations (1% outlier columns x20 for W8A8) and a pool of weight copies,
-    generated on the GPU from a seeded device generator."""
-    g = torch.Generator(device=dev).manual_seed(seed)
-    x = torch.randn(m, k, generator=g, device=dev)
+    """BASELINE.json's synthetic operands, generated on the host from one seeded
+    CPU generator (so the GPU run and the CPU baseline see the same values):
+    activations ~N(0,1) in bf16 (W8A8: 1% of the columns x20), weights
+    W ~N(0, 0.02) quantized symmetric per output channel (scale = absmax/127,
+    round-half-even), then moved to `dev` together with a pool of weight copies
+    large enough to defeat the caches."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g)
     if mode == "w8a8":
-        cols = torch.randperm(k, generator=g, device=dev)[: max(1, k // 100)]
+        cols = torch.randperm(k, generator=g)[: max(1, k // 100)]
         x[:, cols] *= 20.0
     x = x.to(torch.bfloat16)
+    w = torch.randn(n, k, generator=g) * 0.02
+    s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+    q = torch.round(w / s[:, None]).clamp_(-127, 127).to(torch.int8)
+    del w
+    if dev is not None and torch.device(dev).type != "cpu":
+        x, q, s = x.to(dev), q.to(dev), s.to(dev)
     wbytes = n * k + 4 * n
     copies = max(2, min(max_copies, math.ceil(pool_bytes / wbytes)))
-    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g, device=dev)
-    s = torch.rand(n, generator=g, device=dev) * 1e-3 + 1e-4
     qs = [q] + [q.clone() for _ in range(copies - 1)]
     ss = [s] + [s.clone() for _ in range(copies - 1)]
     return x, qs, ss
@@ -222,7 +230,7 @@ def sweep_cases():
     return cases
 
 
-def run_sweep(lib, dev, quick=False, tag=""):
+def run_sweep(lib, dev, quick=False, tag="", floor=False):
     from nanovllm.quantization import _hip
     L = Launcher(lib, dev)
     out = []
@@ -231,8 +239,8 @@ def run_sweep(lib, dev, quick=False, tag=""):
         cases = [c for c in cases if c[0] in ("cfg1", "cfg2") or (c[0].startswith("cfg3") and c[1] == "w8a8")]
     # full records go to a file (the JSON line carries a compact form)
     (ROOT / "gpurun_out").mkdir(exist_ok=True)
-    log = open(ROOT / "gpurun_out" / (f"bench_sweep_{tag}.jsonl" if tag else "bench_sweep.jsonl"), "w")
-    for ci, (tag, mode, m, n, k) in enumerate(cases):
+    log = open(sweep_file(tag), "w")
+    for ci, (cfg, mode, m, n, k) in enumerate(cases):
         if ci % 16 == 0:
             print(f"sweep case {ci}/{len(cases)}", file=sys.stderr, flush=True)
         x, qs, ss = make_inputs(mode, m, n, k, dev)
@@ -251,9 +259,9 @@ def run_sweep(lib, dev, quick=False, tag=""):
             tq = None
             path = _hip.select_path(_hip.OP_W8A16, m, n, k)
         r = roofline_for(mode, m, n, k, t)
-        rec = dict(cfg=tag, mode=mode, M=m, N=n, K=k, path=path, us=round(t * 1e6, 3), gbs=round(r["gbs"], 1),
+        rec = dict(cfg=cfg, mode=mode, M=m, N=n, K=k, path=path, us=round(t * 1e6, 3), gbs=round(r["gbs"], 1),
                    tops=round(r["tops"], 2), bound=r["bound"], frac=round(r["frac"], 4), weight_copies=copies)
-        if path.startswith("dma"):
+        if floor and path.startswith("dma"):
             # operand-delivery floor of the same tiles (unsplit), same weight copies
             op = _hip.OP_W8A8 if mode == "w8a8" else _hip.OP_W8A16
             xa = xq if mode == "w8a8" else x
@@ -261,7 +269,7 @@ def run_sweep(lib, dev, quick=False, tag=""):
                 tf = time_kernel(lambda i: L.operand_floor(op, xa, qs[i]), copies)
                 rec["floor_us"] = round(tf * 1e6, 3)
             except RuntimeError as exc:
-                print(f"operand floor not measured for {tag} {mode} {m}x{n}x{k}: {exc}", file=sys.stderr)
+                print(f"operand floor not measured for {cfg} {mode} {m}x{n}x{k}: {exc}", file=sys.stderr)
         if tq is not None:
             rec["act_quant_us"] = round(tq * 1e6, 3)
             rec["act_quant_gbs"] = round(act_quant_bytes(m, k) / tq / 1e9, 1)
@@ -285,10 +293,8 @@ def cpu_baseline(budget_s=12.0):
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     m, n, k = HEADLINE["m"], HEADLINE["n"], HEADLINE["k"]
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
-    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g)
-    s = torch.rand(n, generator=g) * 1e-3 + 1e-4
+    x, qs, ss = make_inputs("w8a8", m, n, k, "cpu", pool_bytes=0)   # the GPU headline's own operands
+    q, s = qs[0], ss[0]
 
     def step():
         xq, a_s = oracle.quantize_rows_torch(x)
@@ -307,7 +313,8 @@ def cpu_baseline(budget_s=12.0):
     nbytes = w8a8_gemm_bytes(m, n, k) + act_quant_bytes(m, k)
     return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=threads, kind="port",
                 ms_per_step=round(med * 1e3, 3),
-                sample=f"{len(times)} steps of the headline W8A8 linear (M={m}, N={n}, K={k}), "
+                sample=f"{len(times)} steps of the headline W8A8 linear (M={m}, N={n}, K={k}, the GPU run's seeded "
+                       f"inputs), "
                        f"median, torch CPU {torch.__version__} with {threads} threads, ~{budget_s:.0f}s budget")
 
 
@@ -341,21 +348,39 @@ def run_profile_case(spec):
 
 # ---------------------------------------------------------------- config 5 (end to end)
 
+def _child(cmd, timeout_s):
+    """Run `cmd` as a child process (stdout and stderr to this stderr); returns
+    None on success, else a short error string. Never raises."""
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([str(ROOT), str(ROOT / "tiny-vllm_amd"),
+                                                       os.environ.get("PYTHONPATH", "")]))
+    try:
+        proc = subprocess.run(cmd, env=env, stdout=sys.stderr, stderr=sys.stderr, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        return f"timed out after {timeout_s} s"
+    except OSError as exc:
+        return f"could not start: {exc}"
+    if proc.returncode != 0:
+        return f"exit code {proc.returncode}"
+    return None
+
+
 def run_e2e(timeout_s=420):
     """Config 5 through the engine (nanovllm.bench_e2e) in a child process:
     256 sequences, inputs and outputs uniform 100-1024, greedy, bf16 vs W8A16
-    vs W8A8 on a random-init Qwen3-0.6B. Started before this process
-    initialises the GPU; its report comes back through a JSON file."""
+    vs W8A8 on a random-init Qwen3-0.6B. Its report comes back through a JSON
+    file. A failed or timed-out leg is recorded as {"error": ...}; it never
+    costs the headline."""
     out = ROOT / "gpurun_out" / "bench_e2e.json"
     out.parent.mkdir(exist_ok=True)
     if out.exists():
         out.unlink()
-    cmd = [sys.executable, "-m", "nanovllm.bench_e2e", "--modes", "bf16,int8,w8a8", "--output", str(out)]
-    env = dict(os.environ, PYTHONPATH=os.pathsep.join([str(ROOT / "tiny-vllm_amd"), os.environ.get("PYTHONPATH", "")]))
     t0 = time.perf_counter()
-    proc = subprocess.run(cmd, env=env, stdout=sys.stderr, stderr=sys.stderr, timeout=timeout_s)
-    if proc.returncode != 0 or not out.is_file():
-        raise RuntimeError(f"e2e leg failed with exit code {proc.returncode}")
+    err = _child([sys.executable, "-m", "nanovllm.bench_e2e", "--modes", "bf16,int8,w8a8", "--output", str(out)],
+                 timeout_s)
+    if err is None and not out.is_file():
+        err = "no report written"
+    if err is not None:
+        return dict(error=f"e2e leg failed: {err}", leg_seconds=round(time.perf_counter() - t0, 1))
     rep = json.loads(out.read_text())
     res = {}
     for r in rep["results"]:
@@ -374,6 +399,27 @@ def run_e2e(timeout_s=420):
                        "greedy, max_num_batched_tokens 16384, HIP-graph decode")
     res["leg_seconds"] = round(time.perf_counter() - t0, 1)
     return res
+
+
+def sweep_file(tag):
+    return ROOT / "gpurun_out" / (f"bench_sweep_{tag}.jsonl" if tag else "bench_sweep.jsonl")
+
+
+def run_sweep_child(quick, tag, floor, timeout_s=480):
+    """Configs 1-4 in a child process (`bench.py --sweep-only`), so that a
+    failure there is recorded instead of losing the headline. Returns
+    (records, error): the records the child completed, and None or an error."""
+    path = sweep_file(tag)
+    path.parent.mkdir(exist_ok=True)
+    if path.exists():
+        path.unlink()
+    cmd = [sys.executable, str(ROOT / "bench.py"), "--sweep-only"] + (["--quick"] if quick else []) \
+        + (["--tag", tag] if tag else []) + (["--floor"] if floor else [])
+    err = _child(cmd, timeout_s)
+    recs = []
+    if path.is_file():
+        recs = [json.loads(line) for line in path.read_text().splitlines() if line.strip()]
+    return recs, (None if err is None else f"sweep leg failed after {len(recs)} cases: {err}")
 
 
 def targets_from(sweep, e2e):
@@ -402,6 +448,20 @@ def compact(sweep):
 
 # ---------------------------------------------------------------- main
 
+KERNEL_SOURCES = ("tiny-vllm_amd/csrc/gemm_dma_kernel.h", "tiny-vllm_amd/csrc/gemm_dma.hip",
+                  "tiny-vllm_amd/csrc/tvq_common.h")
+
+
+def kernel_source_sha():
+    """sha256 (first 16 hex digits) over the W8A8 DMA GEMM's sources: a traffic
+    record measured on other kernel code does not attach to this one."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -413,6 +473,10 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 engine leg")
     ap.add_argument("--tag", default="", help="suffix of the sweep record file (bench_sweep_TAG.jsonl in the output "
                                               "folder), for runs under other kernel switches")
+    ap.add_argument("--floor", action="store_true",
+                    help="also time the DMA tiles' operand stream alone (tvq_gemm_operand_floor) at the headline "
+                         "and for every DMA sweep entry")
+    ap.add_argument("--sweep-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--profile", action="store_true",
                     help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
@@ -431,7 +495,18 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.sweep_only:   # child of the sweep leg: records go to the sweep file, nothing to stdout
+        from nanovllm.quantization import _hip
+        lib = _hip.load_library()
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        run_sweep(lib, dev, quick=args.quick, tag=args.tag, floor=args.floor)
+        return
+
+    # The auxiliary legs run first, each in a child process, before this
+    # process touches the GPU; a failure in either is recorded in the line.
     e2e = None if args.no_e2e else run_e2e()
+    sweep, sweep_err = (None, None) if args.no_sweep else run_sweep_child(args.quick, args.tag, args.floor)
 
     from nanovllm.quantization import _hip
     lib = _hip.load_library()
@@ -481,32 +556,44 @@ def main():
     xq0, a_s0 = _hip.act_quant(x)
     t_gemm = time_kernel(lambda i: L.w8a8(xq0, a_s0, qs[i], ss[i], y), copies, min_launches=256)
     r = roofline_for("w8a8", m, n, k, t_gemm)
+    kernel = _hip.select_path(_hip.OP_W8A8, m, n, k)
     traffic = None
     tfile = ROOT / "profiles" / "traffic_w8a8_gemm_qkv_m256.json"
     if tfile.is_file():
         rec = json.loads(tfile.read_text())
-        if rec.get("kernel") == _hip.select_path(_hip.OP_W8A8, m, n, k):  # only for the kernel it measured
+        # only for the kernel it measured: same path, same kernel source
+        if rec.get("kernel") == kernel and rec.get("kernel_source_sha") == kernel_source_sha():
             traffic = rec.get("hbm_bytes_per_launch")
-    # The same tiles' operand stream alone (no MFMA, no output): the floor that
-    # the GEMM's data movement sets, over the same rotating weight copies.
-    try:
-        t_floor = time_kernel(lambda i: L.operand_floor(_hip.OP_W8A8, xq0, qs[i]), copies, min_launches=256)
-    except RuntimeError as exc:  # auxiliary: the headline line must not depend on it
-        print(f"operand floor not measured: {exc}", file=sys.stderr)
-        t_floor = None
+    t_floor = None
+    if args.floor:
+        # The same tiles' operand stream alone (no MFMA, no output): the floor
+        # that the GEMM's data movement sets, over the same rotating copies.
+        try:
+            t_floor = time_kernel(lambda i: L.operand_floor(_hip.OP_W8A8, xq0, qs[i]), copies, min_launches=256)
+        except RuntimeError as exc:
+            print(f"operand floor not measured: {exc}", file=sys.stderr)
     roof = dict(bound=r["bound"], achieved=round(r["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
                 frac=round(r["gbs"] / PEAK_HBM_GBS, 4), traffic=traffic,
-                kernel=_hip.select_path(_hip.OP_W8A8, m, n, k), kernel_us=round(t_gemm * 1e6, 3),
+                kernel=kernel, kernel_us=round(t_gemm * 1e6, 3),
                 algorithmic_bytes=r["bytes"], tops=round(r["tops"], 3),
                 operand_floor_us=None if t_floor is None else round(t_floor * 1e6, 3),
                 floor_over_kernel=None if t_floor is None else round(t_floor / t_gemm, 4))
     del x, qs, ss
     torch.cuda.empty_cache()
 
-    sweep = None if args.no_sweep else run_sweep(lib, dev, quick=args.quick, tag=args.tag)
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline()
+        except Exception as exc:  # reported baseline only: never costs the headline
+            cpu = dict(error=f"cpu baseline failed: {type(exc).__name__}: {exc}")
 
-    line = {
+    print(json.dumps(build_line(args, value, t_step, m, n, k, copies, roof, cpu, sweep, sweep_err, e2e)), flush=True)
+
+
+def build_line(args, value, t_step, m, n, k, copies, roof, cpu, sweep, sweep_err, e2e):
+    """The one JSON line (the driver's contract) from the measured pieces."""
+    return {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
@@ -518,7 +605,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,1) activations with 1% outlier columns x20; random int8 weights)",
+        "data": "synthetic (seeded N(0,1) activations with 1% outlier columns x20; N(0,0.02) weights quantized "
+                "per output channel to int8)",
         "config": {
             "workload": "W8A8 linear = per-token act-quant + int8 MFMA GEMM, Qwen3-0.6B qkv_proj "
                         f"N={n} K={k}, M={m} tokens (BASELINE configs[1]); {copies} rotating weight copies "
@@ -530,8 +618,8 @@ def main():
         "targets": targets_from(sweep, e2e),
         "e2e": e2e,
         "sweep": None if sweep is None else compact(sweep),
+        "sweep_error": sweep_err,
     }
-    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

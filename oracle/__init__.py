@@ -270,6 +270,8 @@ def c_lib() -> ctypes.CDLL:
         lib.oracle_f32_to_bf16.argtypes = [vp, i64, vp]
         lib.oracle_w8a16_rounded_weights.argtypes = [vp, vp, i32, i64, i64, vp]
         lib.oracle_f32_to_f16.argtypes = [vp, i64, vp]
+        lib.oracle_quant_code_sweep.argtypes = [i32, ctypes.c_float, i32, ctypes.POINTER(ctypes.c_int64)]
+        lib.oracle_quant_code_sweep.restype = ctypes.c_int64
         for f in (lib.oracle_act_quant, lib.oracle_quant_f32, lib.oracle_gemm_i32, lib.oracle_w8a8_epilogue,
                   lib.oracle_w8a16_f64, lib.oracle_f32_to_bf16, lib.oracle_w8a16_rounded_weights,
                   lib.oracle_f32_to_f16):
@@ -348,6 +350,15 @@ def c_w8a16_rounded_weights(q: np.ndarray, s: np.ndarray, is_bf16: bool = True) 
     out = np.empty((n, k), np.uint16)
     c_lib().oracle_w8a16_rounded_weights(_p(q), _p(s), int(is_bf16), n, k, _p(out))
     return out
+
+
+def c_quant_code_sweep(is_bf16: bool, variant: int = 0, eps: float = 1e-8) -> tuple[int, int]:
+    """(mismatches, pairs) of the divide-free per-token code against
+    rint(x / s) over every finite non-negative 16-bit (x <= amax) pair
+    (oracle_quant_code_sweep)."""
+    pairs = ctypes.c_int64(0)
+    bad = c_lib().oracle_quant_code_sweep(int(is_bf16), eps, variant, ctypes.byref(pairs))
+    return int(bad), int(pairs.value)
 
 
 def c_f32_to_f16(x: np.ndarray) -> np.ndarray:

@@ -16,6 +16,8 @@
  *   oracle_w8a16_f64       nanovllm/quantization/cuda.py:293-300 with the
  *                          weight scale applied in exact arithmetic:
  *                          y = sum_k x[m,k]*q[n,k] * s[n] + b[n] in double
+ *   oracle_quant_code_sweep utils.py:28-32 again: an exhaustive check that
+ *                          the product's divide-free code equals rint(x / s)
  *
  * Pinned by: tests/test_oracle.py (closed-form special cases, numpy and
  * torch restatements, brute force on tiny inputs, invariants).
@@ -187,4 +189,44 @@ void oracle_f32_to_f16(const float* x, int64_t n, uint16_t* out) {
 /* float -> bf16 RNE over an array (exposed so the tests can pin it). */
 void oracle_f32_to_bf16(const float* x, int64_t n, uint16_t* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(x[i]);
+}
+
+/* Exhaustive check of the product's divide-free per-token code against the
+ * reference's rint(x / s) (utils.py:28-32; IEEE RN divide, ties-to-even).
+ * The product (the act-quant and producer kernels) computes, with
+ * rs = RN(1 / s),
+ *   variant 0:  d = RN(x * rs);  q = fma(fma(-d, s, x), rs, d);  code = rint(q)
+ *   variant 1:  code = rint(RN(x * rs))   (the plain form, known to differ)
+ * and both are odd in x, so non-negative x covers every input. For every
+ * finite non-negative 16-bit (bf16 or fp16) row maximum amax and every finite
+ * non-negative 16-bit x <= amax, with s = max(RN(amax / 127), eps), count the
+ * pairs whose code differs from clamp(rint(RN(x / s)), -127, 127).
+ * Returns the mismatch count; *pairs gets the number of pairs checked. */
+int64_t oracle_quant_code_sweep(int is_bf16, float eps, int variant, int64_t* pairs) {
+  const uint16_t top = is_bf16 ? 0x7f80u : 0x7c00u; /* first non-finite pattern */
+  int64_t bad = 0, n = 0;
+#pragma omp parallel for schedule(dynamic, 64) reduction(+ : bad, n)
+  for (int32_t a = 0; a < (int32_t)top; ++a) {
+    const float amax = is_bf16 ? bf16_to_f32((uint16_t)a) : f16_to_f32((uint16_t)a);
+    float s = amax / 127.0f;
+    if (s < eps) s = eps;
+    const float rs = 1.0f / s;
+    for (int32_t b = 0; b <= a; ++b) {
+      const float x = is_bf16 ? bf16_to_f32((uint16_t)b) : f16_to_f32((uint16_t)b);
+      float want = rintf(x / s);
+      if (want > 127.0f) want = 127.0f;
+      float got;
+      if (variant == 0) {
+        const float d = x * rs;
+        got = rintf(fmaf(fmaf(-d, s, x), rs, d));
+      } else {
+        got = rintf(x * rs);
+      }
+      if (got > 127.0f) got = 127.0f;
+      bad += (got != want);
+      n += 1;
+    }
+  }
+  *pairs = n;
+  return bad;
 }

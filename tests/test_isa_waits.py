@@ -157,3 +157,42 @@ def test_skinny_run_issues_all_loads_before_its_mfmas(skinny_assembly):
         assert loads >= (16 if w8a8 else 24), (name, loads)
         checked += 1
     assert checked >= 4
+
+
+@pytest.fixture(scope="module")
+def floor_assembly(tmp_path_factory):
+    """gfx950 assembly of gemm_dma.hip, which instantiates the operand-floor
+    kernels (kDmaOnly) for every DMA configuration."""
+    hipcc = _hipcc()
+    if hipcc is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa_floor") / "dma.s"
+    src = ROOT / "tiny-vllm_amd" / "csrc" / "gemm_dma.hip"
+    cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    lines = out.read_text().split("\n")
+    starts = [i for i, l in enumerate(lines) if l.startswith("_ZN3tvq3dma15gemm_dma_kernel") and ": " in l]
+    starts.append(len(lines))
+    return {lines[a].split(":")[0]: [l.strip() for l in lines[a:b] if l.strip() and not l.strip().startswith(";")]
+            for a, b in zip(starts, starts[1:])}
+
+
+def test_operand_floor_kernels_touch_only_the_operands(floor_assembly):
+    """The operand-floor kernels get null scale, bias and output pointers: their
+    only vector-memory instructions must be the operand DMA into LDS
+    (global_load_lds_*), with no other global, buffer, flat or scratch access."""
+    checked = 0
+    for name, code in floor_assembly.items():
+        # non-type template arguments after T: kW8A8, kRaw, BM, BN, WM, WN, S, MF, KS, kSplit, kNtW, kGlu, kRot,
+        # kDmaOnly (index 13), ...
+        targs = re.findall(r"L[bi](\d+)E", name.split("gemm_dma_kernelI", 1)[1])
+        if targs[13] != "1":
+            continue
+        vmem = [l.split()[0] for l in code if re.match(r"(global|buffer|flat|scratch)_", l)]
+        bad = sorted({op for op in vmem if not op.startswith("global_load_lds_")})
+        assert not bad, (name, bad)
+        assert vmem, name
+        checked += 1
+    assert checked >= 13 * 2, checked   # every DmaCfg, unsplit and non-temporal-weight variants

@@ -481,3 +481,17 @@ def test_c_f16_rounding_matches_numpy():
     with np.errstate(over="ignore"):
         want = x.astype(np.float16).view(np.uint16)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("is_bf16", [True, False], ids=["bf16", "fp16"])
+def test_divide_free_quant_code_is_exact_for_every_input(is_bf16):
+    """The act-quant and producer kernels compute the per-token code without a
+    divide (csrc/tvq_common.h quant_code: d = x*rs, one fma correction, rint).
+    Over every finite non-negative 16-bit pair x <= amax (the code is odd in x)
+    with s = max(amax/127, 1e-8), it must equal utils.py:28-32's
+    rint(x / s) exactly; the plain rint(x * rs) must not (so the check can fail)."""
+    bad, pairs = oracle.c_quant_code_sweep(is_bf16, variant=0)
+    assert pairs == (532701120 if is_bf16 else 503856640)
+    assert bad == 0
+    plain_bad, _ = oracle.c_quant_code_sweep(is_bf16, variant=1)
+    assert plain_bad > 1000

@@ -123,15 +123,17 @@ bool prefill_w4() {
   return env != nullptr && env[0] == '1';
 }
 
-DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
-  if (streamk_shape(M)) {
+// opt_in: whether the opt-in switches (TVQ_STREAMK, TVQ_PREFILL_W4) may
+// change the tile; the rounded-dequant mode keeps the default tiles.
+DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K, bool opt_in = true) {
+  if (opt_in && streamk_shape(M)) {
     // the widest decode tiles: activation traffic per weight byte 2M/BN (W8A16), M/BN (W8A8)
     if (w8a8) return M > 32 ? DmaCfg::kI8_64x128 : DmaCfg::kI8_32x64;
     return M > 32 ? DmaCfg::kH_64x128w8 : (M > 16 ? DmaCfg::kH_32x64 : DmaCfg::kH_16x128);
   }
   const bool split = split_shape(M, N, K);
   if (w8a8) {
-    if (tiles(M, N, 256, 256) >= 256) return prefill_w4() ? DmaCfg::kI8_256x256w4 : DmaCfg::kI8_256x256;
+    if (tiles(M, N, 256, 256) >= 256) return opt_in && prefill_w4() ? DmaCfg::kI8_256x256w4 : DmaCfg::kI8_256x256;
     if (tiles(M, N, 256, 128) >= 200) return DmaCfg::kI8_256x128;
     if (M > 256 || (split && M > 32)) return DmaCfg::kI8_64x64;
     if (M > 32 && M <= 64 && N >= 16384) return DmaCfg::kI8_64x128;
@@ -141,7 +143,7 @@ DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K) {
     if (M > 64 && tiles(M, N, 64, 64) >= 256) return DmaCfg::kI8_64x64;
     return DmaCfg::kI8_32x64;
   }
-  if (tiles(M, N, 128, 256) >= 200) return prefill_w4() ? DmaCfg::kH_128x256w4 : DmaCfg::kH_128x256;
+  if (tiles(M, N, 128, 256) >= 200) return opt_in && prefill_w4() ? DmaCfg::kH_128x256w4 : DmaCfg::kH_128x256;
   if (M > 256) return DmaCfg::kH_64x128;
   if (M <= 64) {
     if (split && M > 32) return DmaCfg::kH_64x64;
@@ -326,10 +328,8 @@ hipError_t dq_of(const GemmArgs& a, hipStream_t s) {
 
 template <typename T>
 hipError_t dq_t(const GemmArgs& a, hipStream_t s) {
-  switch (choose(false, a.M, a.N, a.K)) {
+  switch (choose(false, a.M, a.N, a.K, /*opt_in=*/false)) {
     case DmaCfg::kH_128x256: return dq_of<T, DmaCfg::kH_128x256>(a, s);
-    case DmaCfg::kH_128x256w4: return dq_of<T, DmaCfg::kH_128x256w4>(a, s);
-    case DmaCfg::kH_16x128: return dq_of<T, DmaCfg::kH_16x128>(a, s);
     case DmaCfg::kH_64x128: return dq_of<T, DmaCfg::kH_64x128>(a, s);
     case DmaCfg::kH_32x64: return dq_of<T, DmaCfg::kH_32x64>(a, s);
     case DmaCfg::kH_64x128w8: return dq_of<T, DmaCfg::kH_64x128w8>(a, s);

@@ -27,7 +27,6 @@ constexpr int64_t kWsBytes = (16 << 20) + (64 << 10);
 constexpr int64_t kXqMaxBytes = TVQ_NOALLOC_MAX_XQ_BYTES;
 constexpr int64_t kMaxRows = TVQ_NOALLOC_MAX_ROWS;
 constexpr int64_t kScratchBytes = kWsBytes + kXqMaxBytes + kMaxRows * 4;
-constexpr int64_t kCounterBytes = 64 << 10;  // the workspace's leading counter block
 static_assert(kWsBytes % 256 == 0 && kXqMaxBytes % 256 == 0, "regions stay 256-byte aligned");
 
 __device__ __align__(256) char scratch[kScratchBytes];
@@ -36,15 +35,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 char* g_scratch[kMaxDevices] = {};
 
-__global__ void clear_words(int* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
 // Address of the current device's scratch array (looked up once per device).
-// The first call also clears the split-K counter block with a small kernel on
-// `stream` (no memset node, so the call may be captured into a graph).
-int device_scratch(char** out, hipStream_t stream) {
+// Nothing is cleared: a file-scope __device__ array is zero when the code
+// object loads, and the split-K fixup's last arriver resets each tile counter
+// it used, so the counter block is zero again after every completed call
+// (the codes and scales are fully rewritten by each call's act-quant).
+int device_scratch(char** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return tvq::report_error(TVQ_E_HIP, "tvq_w8a8_linear_noalloc: no current HIP device");
@@ -54,10 +50,6 @@ int device_scratch(char** out, hipStream_t stream) {
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
       return tvq::report_error(TVQ_E_HIP, "tvq_w8a8_linear_noalloc: hipGetSymbolAddress(scratch) failed");
-    constexpr int words = (int)(kCounterBytes / 4);
-    hipLaunchKernelGGL(clear_words, dim3((words + 255) / 256), dim3(256), 0, stream, static_cast<int*>(p), words);
-    if (hipGetLastError() != hipSuccess)
-      return tvq::report_error(TVQ_E_HIP, "tvq_w8a8_linear_noalloc: clearing the scratch counters failed");
     g_scratch[dev] = static_cast<char*>(p);
   }
   *out = g_scratch[dev];
@@ -77,7 +69,7 @@ extern "C" int tvq_w8a8_linear_noalloc(const void* x, int dtype, const int8_t* q
   if (M == 0) return tvq_w8a8_linear(x, dtype, qweight, w_scales, bias, y, M, N, K, nullptr, nullptr, nullptr, 0,
                                      stream);
   char* base = nullptr;
-  if (int rc = device_scratch(&base, (hipStream_t)stream)) return rc;
+  if (int rc = device_scratch(&base)) return rc;
   int8_t* xq = reinterpret_cast<int8_t*>(base + kWsBytes);
   float* a_scales = reinterpret_cast<float*>(base + kWsBytes + kXqMaxBytes);
   return tvq_w8a8_linear(x, dtype, qweight, w_scales, bias, y, M, N, K, xq, a_scales, base, kWsBytes, stream);

@@ -177,11 +177,11 @@ __device__ __forceinline__ float epi_w8a16_nb(float acc, float s) { return __bui
 //   d = RN(x * rs)            within about one ulp of x / s
 //   r = fma(-d, s, x)         the remainder x - d*s, exact in fp32
 //   q = fma(r, rs, d)         one correction step (Markstein)
-// rint(q) equals rint(RN(x / s)): checked on the CPU with the host's fmaf for
-// 1.63e9 (bf16 x, s) pairs and 6.3e8 (fp16 x, s) pairs -- every input value
-// |x| <= amax for 100000 / 40000 random row maxima -- with no mismatch, where
-// rint(d) alone mismatched 12110 / 11058 times; and on the GPU against the
-// oracle on rows built to sit on and around half-integers. |x / s| <= 127
+// rint(q) equals rint(RN(x / s)) for every finite bf16 and fp16 pair x <= amax
+// with s = max(RN(amax / 127), eps) (the code is odd in x): 5.3e8 bf16 and
+// 5.0e8 fp16 pairs checked exhaustively on the CPU with a correctly rounded
+// fmaf (oracle_quant_code_sweep, run by tests/test_oracle.py), with no
+// mismatch, where rint(d) alone mismatches 3544 / 8365 times. |x / s| <= 127
 // (1 + 2^-23) by the choice of s, so the clamp only guards non-finite rows.
 __device__ __forceinline__ float quant_code(float x, float s, float rs) {
   const float d = x * rs;
