@@ -1,0 +1,186 @@
+"""Every kernel family on the AddressSanitizer build of the CPU emulation
+(test infrastructure; run by tests/test_cpu_emu_kernels.py in a child process
+with the ASan runtime preloaded). Every buffer is a CPU tensor of exactly
+its size, so a read or write past any input, output, workspace or dynamic
+LDS allocation aborts the process. Prints "all cases passed" at the end."""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path[:0] = [str(ROOT), str(ROOT / "tiny-vllm_amd"), str(HERE)]
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+import emu  # noqa: E402
+import oracle  # noqa: E402
+from tests.helpers import bits16, make_activations, make_weights  # noqa: E402
+
+CFG = dict(kI8_256x256=0, kI8_256x128=1, kI8_64x64=2, kI8_64x128=3, kI8_32x64=4, kH_128x256=5, kH_64x128=6,
+           kH_64x64=7, kH_32x64=8, kH_64x128w8=9, kI8_256x256w4=10, kH_128x256w4=11, kH_16x128=12)
+
+
+class _NoDevice:
+    def __init__(self, *a, **k):
+        pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False
+
+
+def main() -> None:
+    lib = emu.load(asan=True)
+    from nanovllm.quantization import _hip
+    n_ws = lib.tvq_gemm_workspace_bytes()
+    raw = torch.zeros(n_ws + 256, dtype=torch.uint8)
+    off = (-raw.data_ptr()) % 256
+    ws = raw[off:off + n_ws]
+    _hip.load_library = lambda: lib
+    _hip._require_gpu = lambda *ts: torch.device("cpu")
+    _hip._stream = lambda dev: None
+    _hip.gemm_workspace = lambda dev: ws
+    torch.cuda.device = _NoDevice
+    force = ctypes.c_int.in_dll(lib, "tvq_test_force_dma_cfg")
+
+    def case(name):
+        print("CASE", name, flush=True)
+
+    # act-quant: vector (1, 2 and 4 waves per row) and scalar paths
+    for m, k in [(3, 1024), (600, 64), (1030, 64), (5, 100), (2, 16384)]:
+        case(f"act_quant {m}x{k}")
+        x = make_activations(m, k, seed=m)
+        q, s = _hip.act_quant(x)
+        rq, rs = oracle.c_act_quant(bits16(x))
+        assert np.array_equal(q.numpy(), rq) and np.array_equal(s.numpy(), rs)
+
+    # GEMMs through the default dispatch (GEMV, skinny, DMA, split-K, generic)
+    for m, n, k in [(1, 64, 2048), (2, 72, 1024), (9, 96, 256), (40, 136, 512), (64, 128, 4096), (300, 130, 1024),
+                    (7, 33, 40), (17, 16384, 128)]:
+        case(f"gemm {m}x{n}x{k}")
+        x = make_activations(m, k, seed=n)
+        q, s = make_weights(n, k, seed=k)
+        bias = torch.randn(n).to(torch.bfloat16)
+        _hip.w8a16_gemm(x, q, s, bias)
+        _hip.w8a16_gemm_rounded(x, q, s, bias)
+        y = _hip.w8a8_linear(x, q, s, bias)
+        assert torch.isfinite(y.float()).all()
+        xq, a_s = oracle.c_act_quant(bits16(x))
+        acc = _hip.w8a8_gemm_i32(torch.from_numpy(xq), q)
+        assert np.array_equal(acc.numpy(), oracle.c_gemm_i32(xq, q.numpy()))
+
+    # every DMA tile configuration, ragged, one and several tiles per workgroup
+    for name, c in CFG.items():
+        bm = int(name.split("_")[1].split("x")[0])
+        bn = int(name.split("x")[1].rstrip("w48"))
+        for cus in ("256", "3"):
+            os.environ["EMU_CUS"] = cus
+            force.value = c
+            m, n, k = bm + bm // 2 + 3, 2 * bn + 40, 384
+            case(f"dma {name} cus={cus} {m}x{n}x{k}")
+            x = make_activations(m, k, seed=c)
+            q, s = make_weights(n, k, seed=c + 1)
+            if name.startswith("kI8"):
+                xq, a_s = _hip.act_quant(x)
+                _hip.w8a8_gemm(xq, a_s, q, s, torch.randn(n).to(torch.bfloat16), torch.bfloat16, split_k=False)
+                _hip.gemm_operand_floor(_hip.OP_W8A8, xq, q)
+            else:
+                _hip.w8a16_gemm(x, q, s, torch.randn(n).to(torch.bfloat16), split_k=False)
+                _hip.gemm_operand_floor(_hip.OP_W8A16, x, q)
+            force.value = -1
+    os.environ["EMU_CUS"] = "256"
+
+    # stream-K (opt-in)
+    os.environ["TVQ_STREAMK"] = "1"
+    os.environ["TVQ_STREAMK_MIN"] = "2"
+    os.environ["EMU_CUS"] = "5"
+    for m, n, k in [(1, 512, 1024), (16, 384, 2048), (33, 1280, 512)]:
+        case(f"streamk {m}x{n}x{k}")
+        x = make_activations(m, k, seed=m)
+        q, s = make_weights(n, k, seed=n)
+        _hip.w8a16_gemm(x, q, s)
+        _hip.w8a8_linear(x, q, s)
+    for v in ("TVQ_STREAMK", "TVQ_STREAMK_MIN"):
+        del os.environ[v]
+    os.environ["EMU_CUS"] = "256"
+
+    # producers and the gate_up epilogue
+    for m, k in [(7, 1024), (600, 256), (9, 1003)]:
+        case(f"producers {m}x{k}")
+        x = make_activations(m, k, seed=k)
+        res = make_activations(m, k, seed=k + 1)
+        _hip.rmsnorm(x, torch.ones(k, dtype=torch.bfloat16), 1e-6, residual=res, out=True, quant=True)
+        _hip.silu_mul(make_activations(m, 2 * k, seed=m), out=True, quant=True)
+    case("glu")
+    from nanovllm.quantization.utils import quantize_int8_per_channel
+    qw, s = quantize_int8_per_channel(torch.randn(320, 384) * 0.02)
+    xq, a_s = _hip.act_quant(make_activations(300, 384, seed=1))
+    q2, s2 = _hip.glu_interleave(qw, s.float())
+    _hip.w8a8_gemm_glu(xq, a_s, q2, s2)
+
+    # no-alloc entry
+    case("noalloc")
+    x = make_activations(8, 1024, seed=3)
+    q, s = make_weights(128, 1024, seed=4)
+    y = torch.empty(8, 128, dtype=torch.bfloat16)
+    assert lib.tvq_w8a8_linear_noalloc(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None, y.data_ptr(), 8, 128, 1024,
+                                       None) == 0
+
+    # attention and q/k-norm + rotary (exactly sized caches and tensors)
+    d = 128
+    for hq, hkv in [(4, 2), (8, 2), (2, 2), (6, 2)]:
+        case(f"prefill_attention {hq}/{hkv}")
+        lens = [1, 65, 129]
+        t = sum(lens)
+        q = torch.randn(t, hq, d).to(torch.bfloat16)
+        k = torch.randn(t, hkv, d).to(torch.bfloat16)
+        v = torch.randn(t, hkv, d).to(torch.bfloat16)
+        offs, o = [], 0
+        for n in lens:
+            offs.append((o, n))
+            o += n
+        blocks = _hip.prefill_blocks(offs)
+        out = torch.empty_like(q)
+        assert lib.tvq_prefill_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0), blocks.data_ptr(),
+                                         blocks.shape[0], hq, hkv, d, 0.088, out.data_ptr(), 1, None) == 0
+    for hq, hkv in [(16, 8), (16, 4)]:
+        case(f"decode_attention {hq}/{hkv}")
+        n_slots, max_len, b = 3, 40, 3
+        kc = torch.randn(n_slots, hkv, max_len, d).to(torch.bfloat16)
+        vc = torch.randn_like(kc)
+        q = torch.randn(b, hq, d).to(torch.bfloat16)
+        kn = torch.randn(b, hkv, d).to(torch.bfloat16)
+        vn = torch.randn(b, hkv, d).to(torch.bfloat16)
+        slots = torch.tensor([2, 0, 1], dtype=torch.int32)
+        lens = torch.tensor([1, 40, 17], dtype=torch.int32)
+        out = torch.empty(b, hq, d, dtype=torch.bfloat16)
+        assert lib.tvq_decode_attention(q.data_ptr(), q.stride(0), kn.data_ptr(), kn.stride(0), vn.data_ptr(),
+                                        vn.stride(0), kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), lens.data_ptr(),
+                                        b, hq, hkv, d, n_slots, max_len, 0.088, out.data_ptr(), 1, None) == 0
+    case("qk_norm_rope")
+    t, hq, hkv, max_pos = 5, 4, 2, 64
+    qkv = torch.randn(t, (hq + 2 * hkv) * d).to(torch.bfloat16)
+    pos = torch.tensor([0, 3, 63, 7, 9], dtype=torch.int64)
+    cos = torch.rand(max_pos, d // 2)
+    sin = torch.rand(max_pos, d // 2)
+    kc = torch.zeros(2, hkv, max_pos, d, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    slots = torch.tensor([0, 1, 1, 0, 1], dtype=torch.int64)
+    qo = torch.empty(t, hq, d, dtype=torch.bfloat16)
+    ko = torch.empty(t, hkv, d, dtype=torch.bfloat16)
+    w = torch.ones(d, dtype=torch.bfloat16)
+    assert lib.tvq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                w.data_ptr(), w.data_ptr(), 1e-6, t, hq, hkv, d, max_pos, qo.data_ptr(), ko.data_ptr(),
+                                kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), 2, max_pos, 1, None) == 0
+    print("all cases passed", flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,185 @@
+"""Build the kernel sources of tiny-vllm_amd/csrc for the CPU emulation
+(test infrastructure: hip/hip_runtime.h, emu_runtime.cpp).
+
+The sources are copied unchanged except for four mechanical rewrites that
+host C++ cannot express:
+  * kernel<<<grid, block, shmem, stream>>>(args)  ->  ::emu::launch(&kernel, grid, block, shmem, stream, args)
+  * inline asm: "s_barrier" -> ::emu::barrier(); an LDS wait (lgkmcnt) ->
+    ::emu::wave_barrier(); other waits and register pins dropped
+  * __attribute__((address_space(N))) and the amdgpu_* kernel attributes dropped
+  * extern __shared__ T name[]  ->  T* name = (T*)::emu::dyn_smem()
+and compiled with the host clang into tests/cpu_emu/_build/libtvq_emu[_asan].so,
+which exports the same C ABI as the product library (include/tvq.h).
+
+Usage: python tests/cpu_emu/build.py [--asan]
+"""
+from __future__ import annotations
+
+import argparse
+import re
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+CSRC = ROOT / "tiny-vllm_amd" / "csrc"
+INCLUDE = ROOT / "include"
+BUILD = HERE / "_build"
+CLANG = "/opt/rocm/llvm/bin/clang++"
+
+
+def _match(text: str, i: int, open_c: str, close_c: str) -> int:
+    """Index just past the bracket closing the one at text[i]."""
+    depth = 0
+    j = i
+    while j < len(text):
+        c = text[j]
+        if c == '"':
+            j = text.index('"', j + 1)
+        elif c == open_c:
+            depth += 1
+        elif c == close_c:
+            depth -= 1
+            if depth == 0:
+                return j + 1
+        j += 1
+    raise ValueError("unbalanced")
+
+
+def _rewrite_launches(src: str) -> str:
+    out = []
+    pos = 0
+    while True:
+        i = src.find("<<<", pos)
+        if i < 0:
+            out.append(src[pos:])
+            return "".join(out)
+        # kernel expression: identifier chars / :: and balanced template arguments, backwards
+        j = i
+        while True:
+            if j > 0 and src[j - 1] == ">":
+                depth = 0
+                k = j - 1
+                while k >= 0:
+                    if src[k] == ">":
+                        depth += 1
+                    elif src[k] == "<":
+                        depth -= 1
+                        if depth == 0:
+                            break
+                    k -= 1
+                j = k
+                continue
+            if j > 0 and (src[j - 1].isalnum() or src[j - 1] in "_:"):
+                j -= 1
+                continue
+            break
+        kern = src[j:i]
+        cfg_end = src.index(">>>", i)
+        cfg = src[i + 3:cfg_end]
+        p = cfg_end + 3
+        while src[p].isspace():
+            p += 1
+        assert src[p] == "(", src[i - 40:p + 10]
+        q = _match(src, p, "(", ")")
+        args = src[p + 1:q - 1]
+        out.append(src[pos:j])
+        out.append(f"[&] {{ auto* emu_k = &{kern}; ::emu::launch(emu_k, {cfg}, {args}); }}()")
+        pos = q
+
+
+def _rewrite_asm(src: str) -> str:
+    out = []
+    pos = 0
+    pat = re.compile(r"\basm\b\s*(volatile\s*)?\(")
+    while True:
+        m = pat.search(src, pos)
+        if not m:
+            out.append(src[pos:])
+            return "".join(out)
+        start = m.start()
+        q = _match(src, m.end() - 1, "(", ")")
+        body = src[m.end():q - 1]
+        lit = re.match(r'\s*"([^"]*)"', body)
+        text = lit.group(1) if lit else ""
+        end = q
+        while end < len(src) and src[end].isspace():
+            end += 1
+        if end < len(src) and src[end] == ";":
+            end += 1
+        out.append(src[pos:start])
+        if "s_barrier" in text:
+            out.append("::emu::barrier();")
+        elif "lgkmcnt" in text:
+            out.append("::emu::wave_barrier();")
+        else:
+            out.append(";")
+        pos = end
+
+
+def rewrite(src: str) -> str:
+    src = _rewrite_launches(src)
+    src = _rewrite_asm(src)
+    src = re.sub(r"__attribute__\(\(address_space\(\d\)\)\)", "", src)
+    src = re.sub(r"__attribute__\(\(amdgpu_\w+\((?:[^()]|\([^()]*\))*\)\)\)", "", src)
+    src = re.sub(r"extern\s+__shared__\s+(?:__attribute__\(\(aligned\(\d+\)\)\)\s+)?(\w+)\s+(\w+)\[\]\s*;",
+                 r"\1* \2 = reinterpret_cast<\1*>(::emu::dyn_smem());", src)
+    return src
+
+
+def build(asan: bool = False, jobs: int = 8, csrc: Path = CSRC, include: Path = INCLUDE, name: str = "") -> Path:
+    """Compile `csrc` (default: the package's kernel sources) into the
+    emulation library; `name` gives another library name (e.g. for sources
+    of another revision)."""
+    stage = BUILD / ((name or "src") + ("_asan" if asan else ""))
+    if stage.exists():
+        shutil.rmtree(stage)
+    (stage / "tiny-vllm_amd" / "csrc").mkdir(parents=True)
+    shutil.copytree(include, stage / "include")
+    for f in csrc.iterdir():
+        if f.suffix in (".hip", ".h"):
+            (stage / "tiny-vllm_amd" / "csrc" / (f.stem + (".cpp" if f.suffix == ".hip" else ".h"))).write_text(
+                rewrite(f.read_text()))
+    flags = ["-std=c++17", "-fPIC", "-g", "-O1" if asan else "-O2", "-ffp-contract=off", "-fno-fast-math",
+             "-Wno-unused-value", "-Wno-ignored-attributes", "-Wno-unknown-attributes", "-Wno-unused-command-line-argument",
+             "-DTVQ_TEST_HOOKS", f"-I{HERE}"]
+    if asan:
+        flags += ["-fsanitize=address", "-fno-omit-frame-pointer"]
+    objs = []
+    srcs = sorted((stage / "tiny-vllm_amd" / "csrc").glob("*.cpp")) + [HERE / "emu_runtime.cpp"]
+
+    def cc(s: Path) -> Path:
+        o = stage / (s.stem + ".o")
+        proc = subprocess.run([CLANG, *flags, "-c", str(s), "-o", str(o)], capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"emu build failed for {s.name}:\n{proc.stderr[-6000:]}")
+        return o
+
+    with ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(cc, srcs))
+    lib = BUILD / (f"libtvq_emu{'_' + name if name else ''}{'_asan' if asan else ''}.so")
+    link = [CLANG, "-shared", *(["-fsanitize=address", "-shared-libasan"] if asan else []), "-o", str(lib),
+            *map(str, objs)]
+    proc = subprocess.run(link, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"emu link failed:\n{proc.stderr[-4000:]}")
+    return lib
+
+
+def asan_runtime() -> str:
+    return subprocess.run([CLANG, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                          text=True, check=True).stdout.strip()
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--asan", action="store_true")
+    ap.add_argument("--csrc", type=Path, default=CSRC, help="kernel source folder (default: the package's)")
+    ap.add_argument("--include", type=Path, default=INCLUDE)
+    ap.add_argument("--name", default="", help="library name suffix")
+    a = ap.parse_args()
+    print(build(a.asan, csrc=a.csrc, include=a.include, name=a.name))
+    sys.exit(0)

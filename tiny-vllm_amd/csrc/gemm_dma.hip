@@ -123,9 +123,21 @@ bool prefill_w4() {
   return env != nullptr && env[0] == '1';
 }
 
+#ifdef TVQ_TEST_HOOKS
+// CPU-emulation builds of the tests only (never defined for the GPU library):
+// a DmaCfg index that choose() returns for its own family, so that every tile
+// configuration can be exercised at small shapes.
+extern "C" int tvq_test_force_dma_cfg;
+int tvq_test_force_dma_cfg = -1;
+#endif
+
 // opt_in: whether the opt-in switches (TVQ_STREAMK, TVQ_PREFILL_W4) may
 // change the tile; the rounded-dequant mode keeps the default tiles.
 DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K, bool opt_in = true) {
+#ifdef TVQ_TEST_HOOKS
+  if (tvq_test_force_dma_cfg >= 0 && kInfo[tvq_test_force_dma_cfg].w8a8 == w8a8)
+    return (DmaCfg)tvq_test_force_dma_cfg;
+#endif
   if (opt_in && streamk_shape(M)) {
     // the widest decode tiles: activation traffic per weight byte 2M/BN (W8A16), M/BN (W8A8)
     if (w8a8) return M > 32 ? DmaCfg::kI8_64x128 : DmaCfg::kI8_32x64;

@@ -830,6 +830,9 @@ inline int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+#ifdef TVQ_TEST_HOOKS
+  cus[dev] = 0;  // CPU-emulation builds of the tests: the CU count may change between calls
+#endif
   if (cus[dev] == 0) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
@@ -932,7 +935,8 @@ hipError_t launch_dma(const void* x, const float* a_s, const int8_t* qw, const f
   const int units = tiles * splits;
   const int resident = resident_workgroups(C::kLdsBytes);
   int grid = units;
-  if (resident > 0 && units > resident) grid = resident - resident % 8;  // keep whole XCD rounds
+  // keep whole XCD rounds (8 XCDs), but never round a small device's grid to zero
+  if (resident > 0 && units > resident) grid = resident >= 8 ? resident - resident % 8 : resident;
   kern<<<dim3(grid), dim3(C::kThreads), C::kLdsBytes, stream>>>(x, a_s, qw, ws, static_cast<const uint16_t*>(bias),
                                                                  y, M, N, K, group, m_major, splits,
                                                                  static_cast<char*>(wsp), 0);
