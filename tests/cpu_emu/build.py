@@ -4,8 +4,9 @@
 The sources are copied unchanged except for four mechanical rewrites that
 host C++ cannot express:
   * kernel<<<grid, block, shmem, stream>>>(args)  ->  ::emu::launch(&kernel, grid, block, shmem, stream, args)
-  * inline asm: "s_barrier" -> ::emu::barrier(); an LDS wait (lgkmcnt) ->
-    ::emu::wave_barrier(); other waits and register pins dropped
+  * inline asm: "s_barrier" -> ::emu::barrier(); a vmcnt(N) wait ->
+    ::emu::wait_vm(N); an LDS wait (lgkmcnt) -> ::emu::wave_barrier();
+    register pins dropped
   * __attribute__((address_space(N))) and the amdgpu_* kernel attributes dropped
   * extern __shared__ T name[]  ->  T* name = (T*)::emu::dyn_smem()
 and compiled with the host clang into tests/cpu_emu/_build/libtvq_emu[_asan].so,
@@ -111,12 +112,18 @@ def _rewrite_asm(src: str) -> str:
         if end < len(src) and src[end] == ";":
             end += 1
         out.append(src[pos:start])
+        repl = ""
+        vm = re.search(r"vmcnt\((\d+|%0)\)", text)
+        if vm:
+            n = vm.group(1)
+            if n == "%0":
+                n = re.search(r'"n"\s*\((.*?)\)\s*(?::|$)', body, re.S).group(1)
+            repl += f"::emu::wait_vm({n});"
         if "s_barrier" in text:
-            out.append("::emu::barrier();")
+            repl += "::emu::barrier();"
         elif "lgkmcnt" in text:
-            out.append("::emu::wave_barrier();")
-        else:
-            out.append(";")
+            repl += "::emu::wave_barrier();"
+        out.append(repl or ";")
         pos = end
 
 

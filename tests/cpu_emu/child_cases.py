@@ -1,8 +1,15 @@
-"""Every kernel family on the AddressSanitizer build of the CPU emulation
-(test infrastructure; run by tests/test_cpu_emu_kernels.py in a child process
-with the ASan runtime preloaded). Every buffer is a CPU tensor of exactly
-its size, so a read or write past any input, output, workspace or dynamic
-LDS allocation aborts the process. Prints "all cases passed" at the end."""
+"""A case of every kernel family on the CPU emulation, with parity checks,
+run by tests/test_cpu_emu_kernels.py in child processes (test
+infrastructure), because the emulation's modes are fixed per process:
+
+  --asan   the AddressSanitizer build, with the ASan runtime preloaded. Every
+           buffer is a CPU tensor of exactly its size, so a read or write past
+           any input, output, workspace or dynamic LDS allocation aborts.
+  (plain)  run with EMU_DMA=late (each LDS DMA lands only at its wave's
+           vmcnt wait) and EMU_SHUFFLE=seed (fibers in random order): a
+           missing DMA wait or a cross-wave race shows as a parity failure.
+
+Prints "all cases passed" at the end."""
 from __future__ import annotations
 
 import ctypes
@@ -36,8 +43,25 @@ class _NoDevice:
         return False
 
 
+def _w8a16_ok(y, x, q, s, bias=None) -> None:
+    """Within the GPU tests' bound of the exact fp64 product."""
+    y64 = oracle.c_w8a16_f64(bits16(x), q.numpy(), s.numpy(), None if bias is None else bias.float().numpy(),
+                             is_bf16=x.dtype == torch.bfloat16)
+    mag = (np.abs(x.float().numpy()).astype(np.float64) @ np.abs(q.numpy()).astype(np.float64).T) * s.numpy()[None]
+    bound = np.abs(y64) * 2.0 ** -8 + mag * (x.shape[1] * 2.0 ** -23) + 1e-30
+    assert np.all(np.abs(y.float().numpy().astype(np.float64) - y64) <= bound)
+
+
+def _w8a8_ok(y, xq, a_s, q, s, bias=None) -> None:
+    """Bit-exact against the restated reference epilogue."""
+    xq, a_s = np.asarray(xq), np.asarray(a_s)
+    yb, _ = oracle.c_w8a8_epilogue(oracle.c_gemm_i32(xq, q.numpy()), a_s, s.numpy(),
+                                   None if bias is None else bias.float().numpy())
+    assert np.array_equal(bits16(y), yb)
+
+
 def main() -> None:
-    lib = emu.load(asan=True)
+    lib = emu.load(asan="--asan" in sys.argv)
     from nanovllm.quantization import _hip
     n_ws = lib.tvq_gemm_workspace_bytes()
     raw = torch.zeros(n_ws + 256, dtype=torch.uint8)
@@ -68,11 +92,11 @@ def main() -> None:
         x = make_activations(m, k, seed=n)
         q, s = make_weights(n, k, seed=k)
         bias = torch.randn(n).to(torch.bfloat16)
-        _hip.w8a16_gemm(x, q, s, bias)
+        _w8a16_ok(_hip.w8a16_gemm(x, q, s, bias), x, q, s, bias)
         _hip.w8a16_gemm_rounded(x, q, s, bias)
         y = _hip.w8a8_linear(x, q, s, bias)
-        assert torch.isfinite(y.float()).all()
         xq, a_s = oracle.c_act_quant(bits16(x))
+        _w8a8_ok(y, xq, a_s, q, s, bias)
         acc = _hip.w8a8_gemm_i32(torch.from_numpy(xq), q)
         assert np.array_equal(acc.numpy(), oracle.c_gemm_i32(xq, q.numpy()))
 
@@ -87,12 +111,14 @@ def main() -> None:
             case(f"dma {name} cus={cus} {m}x{n}x{k}")
             x = make_activations(m, k, seed=c)
             q, s = make_weights(n, k, seed=c + 1)
+            bias = torch.randn(n).to(torch.bfloat16)
             if name.startswith("kI8"):
                 xq, a_s = _hip.act_quant(x)
-                _hip.w8a8_gemm(xq, a_s, q, s, torch.randn(n).to(torch.bfloat16), torch.bfloat16, split_k=False)
+                y = _hip.w8a8_gemm(xq, a_s, q, s, bias, torch.bfloat16, split_k=False)
+                _w8a8_ok(y, xq, a_s, q, s, bias)
                 _hip.gemm_operand_floor(_hip.OP_W8A8, xq, q)
             else:
-                _hip.w8a16_gemm(x, q, s, torch.randn(n).to(torch.bfloat16), split_k=False)
+                _w8a16_ok(_hip.w8a16_gemm(x, q, s, bias, split_k=False), x, q, s, bias)
                 _hip.gemm_operand_floor(_hip.OP_W8A16, x, q)
             force.value = -1
     os.environ["EMU_CUS"] = "256"
@@ -105,8 +131,9 @@ def main() -> None:
         case(f"streamk {m}x{n}x{k}")
         x = make_activations(m, k, seed=m)
         q, s = make_weights(n, k, seed=n)
-        _hip.w8a16_gemm(x, q, s)
-        _hip.w8a8_linear(x, q, s)
+        _w8a16_ok(_hip.w8a16_gemm(x, q, s), x, q, s)
+        xq, a_s = oracle.c_act_quant(bits16(x))
+        _w8a8_ok(_hip.w8a8_linear(x, q, s), xq, a_s, q, s)
     for v in ("TVQ_STREAMK", "TVQ_STREAMK_MIN"):
         del os.environ[v]
     os.environ["EMU_CUS"] = "256"
@@ -123,7 +150,8 @@ def main() -> None:
     qw, s = quantize_int8_per_channel(torch.randn(320, 384) * 0.02)
     xq, a_s = _hip.act_quant(make_activations(300, 384, seed=1))
     q2, s2 = _hip.glu_interleave(qw, s.float())
-    _hip.w8a8_gemm_glu(xq, a_s, q2, s2)
+    yref, _ = _hip.silu_mul(_hip.w8a8_gemm(xq, a_s, qw, s.float(), out_dtype=torch.bfloat16, split_k=False))
+    assert torch.equal(_hip.w8a8_gemm_glu(xq, a_s, q2, s2), yref)
 
     # no-alloc entry
     case("noalloc")

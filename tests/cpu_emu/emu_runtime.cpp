@@ -4,6 +4,8 @@
 #include <sys/mman.h>
 #include <ucontext.h>
 
+#include <deque>
+#include <random>
 #include <vector>
 
 #include "hip/hip_runtime.h"
@@ -42,6 +44,27 @@ struct Block {
   const void* sched_stack_bottom = nullptr;
   size_t sched_stack_size = 0;
 };
+
+struct DmaOp {
+  char* dst;
+  const char* src;
+  int size;  // -1: the start of one wave instruction (one vm op)
+};
+std::vector<std::deque<DmaOp>> g_dma;  // per wave of the running workgroup
+
+void dma_flush_wave(int w, int keep_ops) {
+  std::deque<DmaOp>& q = g_dma[w];
+  int ops = 0;
+  for (const DmaOp& d : q) ops += d.size < 0;
+  while (ops > keep_ops && !q.empty()) {
+    q.pop_front();  // instruction marker
+    --ops;
+    while (!q.empty() && q.front().size >= 0) {
+      memcpy(q.front().dst, q.front().src, q.front().size);
+      q.pop_front();
+    }
+  }
+}
 
 Block* g_blk = nullptr;
 Fiber* g_cur = nullptr;
@@ -87,9 +110,16 @@ void run_block(Block& b) {
     makecontext(&f.ctx, fiber_entry, 0);
   }
   const int nwaves = (b.n + 63) / 64;
+  g_dma.assign(nwaves, {});
+  static const char* shuffle = getenv("EMU_SHUFFLE");
+  static std::mt19937 rng(shuffle ? (unsigned)atoi(shuffle) : 0u);
+  std::vector<int> order(b.n);
+  for (int i = 0; i < b.n; ++i) order[i] = i;
   for (;;) {
     bool ran = false;
-    for (int i = 0; i < b.n; ++i) {
+    if (shuffle) std::shuffle(order.begin(), order.end(), rng);
+    for (int oi = 0; oi < b.n; ++oi) {
+      const int i = order[oi];
       if (F[i].lane.state != kRun) continue;
       g_cur = &F[i];
 #ifdef EMU_ASAN
@@ -133,7 +163,10 @@ void run_block(Block& b) {
       if (F[i].lane.state != kDone) ++live;
       if (F[i].lane.state == kBar) ++at_bar;
     }
-    if (live == 0) break;
+    if (live == 0) {
+      for (int w = 0; w < nwaves; ++w) dma_flush_wave(w, 0);
+      break;
+    }
     if (at_bar == live) {
       for (int i = 0; i < b.n; ++i)
         if (F[i].lane.state == kBar) F[i].lane.state = kRun;
@@ -166,6 +199,17 @@ void wave_sync(WaveFn fn) {
   g_cur->lane.fn = fn;
   g_cur->lane.state = kWave;
   to_sched();
+}
+
+bool dma_late() {
+  static const char* e = getenv("EMU_DMA");
+  return e != nullptr && strcmp(e, "late") == 0;
+}
+
+void dma_enqueue(int wave, char* dst, const char* src, int size) { g_dma[wave].push_back(DmaOp{dst, src, size}); }
+
+void wait_vm(int n) {
+  if (g_cur != nullptr && !g_dma.empty()) dma_flush_wave(g_cur->lane.wave, n);
 }
 
 void set_last_error(hipError_t e) { g_err = e; }

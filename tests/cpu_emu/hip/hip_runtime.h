@@ -18,8 +18,10 @@
 // (exact for the int8 forms); v_dot2 likewise. exp2 and rcp are the libm
 // results, so those differ from the hardware's by about an ulp. LDS DMA
 // completes when issued (the earliest time the hardware may complete it).
+// With EMU_DMA=late it lands only at the wave's vmcnt wait (the latest).
 // An LDS wait (s_waitcnt lgkmcnt) is a rendezvous of the wave's lanes, which
-// stands in for the hardware's lockstep execution of a wave.
+// stands in for the hardware's lockstep execution of a wave. EMU_SHUFFLE=seed
+// runs the fibers in a seeded random order instead of round-robin.
 #pragma once
 
 #include <math.h>
@@ -120,6 +122,7 @@ inline T get_out(const Lane* l) {
 }
 
 // ---- cross-lane ---------------------------------------------------------
+void wait_vm(int n);
 template <int B>
 void shfl_fn(Lane** L) {  // in[0]: value (B bytes), in[1]: source lane
   unsigned char tmp[64][B];
@@ -222,7 +225,10 @@ inline float __builtin_amdgcn_exp2f(float a) { return exp2f(a); }
 inline float __builtin_amdgcn_rcpf(float a) { return 1.0f / a; }
 // s_waitcnt immediate (gfx9): lgkmcnt in bits 11:8; any wait with lgkmcnt < 15
 // orders this wave's LDS accesses: a wave rendezvous in the emulation
+// and the vmcnt field (bits 3:0 and 15:14) completes this wave's queued DMA.
 inline void __builtin_amdgcn_s_waitcnt(int imm) {
+  const int vm = (imm & 15) | (((imm >> 14) & 3) << 4);
+  if (vm < 63) ::emu::wait_vm(vm);
   if (((imm >> 8) & 15) != 15) ::emu::wave_barrier();
 }
 inline void __builtin_amdgcn_sched_barrier(int) {}
@@ -370,7 +376,14 @@ inline void tr16_fn(Lane** L) {
 }
 
 // global_load_lds: lane l copies `size` bytes from its global address to
-// LDS at (the first active lane's LDS pointer) + offset + l * size.
+// LDS at (the first active lane's LDS pointer) + offset + l * size. In the
+// default mode the copy happens at issue; with EMU_DMA=late it is queued on
+// the wave and lands only when the wave waits for it (s_waitcnt vmcnt), the
+// latest time the hardware may complete it.
+bool dma_late();
+void dma_enqueue(int wave, char* dst, const char* src, int size);
+void wait_vm(int n);  // this wave: complete queued DMA until at most n remain
+
 inline void dma_fn(Lane** L) {
   int first = -1;
   for (int i = 0; i < 64; ++i)
@@ -378,10 +391,15 @@ inline void dma_fn(Lane** L) {
   char* base = get_in<char*>(L[first], 1);
   const int size = get_in<int>(L[first], 2);
   const int off = get_in<int>(L[first], 3);
+  const bool late = dma_late();
+  if (late) dma_enqueue(L[first]->wave, nullptr, nullptr, -1);  // one vm op per instruction
   for (int i = 0; i < 64; ++i) {
     if (!L[i]) continue;
     const char* src = get_in<const char*>(L[i], 0);
-    memcpy(base + off + i * size, src, size);
+    if (late)
+      dma_enqueue(L[first]->wave, base + off + i * size, src, size);
+    else
+      memcpy(base + off + i * size, src, size);
   }
 }
 }  // namespace emu

@@ -11,9 +11,11 @@ against the oracle to the GPU tests' bar:
     GPU tests' bounds (the emulation's exp2 / rcp are libm's, about an ulp
     from the hardware's).
 
-What this does not show: timing, the hardware's asynchronous completion of
-LDS DMA (the emulation completes each DMA op when it is issued), and
-behaviour that depends on several workgroups running at once. Every DMA
+What this does not show: timing, and behaviour that depends on several
+workgroups running at once (one workgroup runs at a time). LDS DMA completes
+at issue here; child processes rerun a case of every family with each DMA
+landing only at its wave's wait and the work-items in random order, and on
+an AddressSanitizer build. Every DMA
 tile configuration is reached at small shapes through a hook compiled into
 the emulation build only (TVQ_TEST_HOOKS), and small CU counts (EMU_CUS) make
 the persistent grid walk several tiles per workgroup.
@@ -564,19 +566,37 @@ def test_prefill_attention(hip, elib, hq, hkv):
     assert ((out.float() - ref).norm() / ref.norm()).item() < 8e-3
 
 
-# ---------------------------------------------------------------- AddressSanitizer
+# ---------------------------------------------------------------- child-process modes
 
-def test_kernels_under_address_sanitizer():
-    """The same kernels built with AddressSanitizer (global buffers sized
-    exactly, dynamic LDS a fresh allocation per workgroup) run a case of every
-    family in a child process: any out-of-bounds access aborts it."""
+def test_kernels_in_child_modes():
+    """Three child processes, run concurrently, each a case of every family:
+
+      * the AddressSanitizer build (global buffers sized exactly, dynamic LDS
+        a fresh allocation per workgroup): any out-of-bounds access aborts;
+      * twice (two seeds) with every LDS DMA landing only at its wave's vmcnt
+        wait, the latest the hardware may complete it, and the work-items in
+        a seeded random order: a stage wait that waits too little, or a
+        cross-wave dependency without a barrier, breaks parity (a stage wait
+        weakened by one stage gives wrong accumulators in this mode and none
+        in the default one)."""
     sys.path.insert(0, str(ROOT / "tests" / "cpu_emu"))
     import build as emu_build
     emu.ensure_built(asan=True)
-    env = dict(os.environ, LD_PRELOAD=emu_build.asan_runtime(),
-               ASAN_OPTIONS="detect_leaks=0:detect_stack_use_after_return=0:abort_on_error=1",
-               PYTHONPATH=os.pathsep.join([str(ROOT), str(ROOT / "tiny-vllm_amd")]))
-    proc = subprocess.run([sys.executable, str(ROOT / "tests" / "cpu_emu" / "asan_cases.py")], env=env,
-                          capture_output=True, text=True, timeout=900)
-    assert proc.returncode == 0, proc.stdout[-3000:] + proc.stderr[-6000:]
-    assert "all cases passed" in proc.stdout
+    emu.ensure_built()
+    base = dict(os.environ, PYTHONPATH=os.pathsep.join([str(ROOT), str(ROOT / "tiny-vllm_amd")]))
+    script = str(ROOT / "tests" / "cpu_emu" / "child_cases.py")
+    runs = {
+        "asan": ([script, "--asan"], dict(base, LD_PRELOAD=emu_build.asan_runtime(),
+                                          ASAN_OPTIONS="detect_leaks=0:detect_stack_use_after_return=0:"
+                                                       "abort_on_error=1")),
+        "late-dma-seed1": ([script], dict(base, EMU_DMA="late", EMU_SHUFFLE="1")),
+        "late-dma-seed2": ([script], dict(base, EMU_DMA="late", EMU_SHUFFLE="2")),
+    }
+    procs = {k: subprocess.Popen([sys.executable, *a], env=e, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                 text=True) for k, (a, e) in runs.items()}
+    failed = []
+    for k, p in procs.items():
+        out, err = p.communicate(timeout=900)
+        if p.returncode != 0 or "all cases passed" not in out:
+            failed.append(f"--- {k}: rc={p.returncode}\n{out[-2000:]}\n{err[-4000:]}")
+    assert not failed, "\n".join(failed)
