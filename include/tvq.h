@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define TVQ_ABI_VERSION 4
+#define TVQ_ABI_VERSION 5
 
 /* Activation / output element types. */
 enum tvq_dtype {
@@ -290,6 +290,40 @@ int tvq_prefill_attention(const void* q, const void* k, const void* v,
                           int64_t v_stride, const int32_t* blocks,
                           int64_t nblocks, int Hq, int Hkv, int head_dim,
                           float scale, void* out, int dtype, void* stream);
+
+/* The attention entry points with o_proj's per-token int8 quantization
+ * fused into the same launch: the W8A8 QuantMethod's quantize_activation of
+ * the attention output (quantize_int8_per_row_dynamic, reference
+ * nanovllm/quantization/utils.py:28-32, applied to o_proj's input in
+ * W8A8QuantMethod.apply, w8a8.py:21-40, called from linear.py:65-68), which
+ * otherwise reads the output back in a separate tvq_act_quant launch.
+ * Arguments as tvq_decode_attention / tvq_prefill_attention, plus
+ *   xq [rows, Hq*head_dim] int8 and a_scales [rows] fp32: exactly what
+ *          tvq_act_quant(out, eps) writes (rows = B, or the prompt tokens)
+ *   counters int32 [counters_len], all zero on entry and left zero on
+ *          return; counters_len >= B (decode) or nblocks (prefill); calls
+ *          sharing a counters array must not overlap
+ * `out` is still written (the quantizer's input). eps > 0; xq 4-byte
+ * aligned. Each token row is quantized by the last of its workgroups to
+ * finish; no workgroup waits for another. */
+int tvq_decode_attention_quant(const void* q, int64_t q_stride,
+                               const void* k_new, int64_t k_stride,
+                               const void* v_new, int64_t v_stride,
+                               void* k_cache, void* v_cache,
+                               const int32_t* slots, const int32_t* lens,
+                               int64_t B, int Hq, int Hkv, int head_dim,
+                               int64_t num_slots, int64_t max_len, float scale,
+                               void* out, int dtype, int8_t* xq,
+                               float* a_scales, float eps, int32_t* counters,
+                               int64_t counters_len, void* stream);
+
+int tvq_prefill_attention_quant(const void* q, const void* k, const void* v,
+                                int64_t v_stride, const int32_t* blocks,
+                                int64_t nblocks, int Hq, int Hkv,
+                                int head_dim, float scale, void* out,
+                                int dtype, int8_t* xq, float* a_scales,
+                                float eps, int32_t* counters,
+                                int64_t counters_len, void* stream);
 
 #ifdef __cplusplus
 }

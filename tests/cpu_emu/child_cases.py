@@ -178,6 +178,18 @@ def main() -> None:
         out = torch.empty_like(q)
         assert lib.tvq_prefill_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0), blocks.data_ptr(),
                                          blocks.shape[0], hq, hkv, d, 0.088, out.data_ptr(), 1, None) == 0
+        case(f"prefill_attention_quant {hq}/{hkv}")
+        out2 = torch.empty_like(q)
+        xq = torch.empty(t, hq * d, dtype=torch.int8)
+        xs = torch.empty(t)
+        cnt = torch.zeros(blocks.shape[0], dtype=torch.int32)
+        assert lib.tvq_prefill_attention_quant(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0),
+                                               blocks.data_ptr(), blocks.shape[0], hq, hkv, d, 0.088,
+                                               out2.data_ptr(), 1, xq.data_ptr(), xs.data_ptr(), 1e-8,
+                                               cnt.data_ptr(), cnt.numel(), None) == 0
+        assert torch.equal(out2.view(torch.int16), out.view(torch.int16))
+        rq, rs = oracle.c_act_quant(bits16(out.view(t, -1)))
+        assert np.array_equal(xq.numpy(), rq) and np.array_equal(xs.numpy(), rs) and int(cnt.abs().sum()) == 0
     for hq, hkv in [(16, 8), (16, 4)]:
         case(f"decode_attention {hq}/{hkv}")
         n_slots, max_len, b = 3, 40, 3
@@ -192,6 +204,19 @@ def main() -> None:
         assert lib.tvq_decode_attention(q.data_ptr(), q.stride(0), kn.data_ptr(), kn.stride(0), vn.data_ptr(),
                                         vn.stride(0), kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), lens.data_ptr(),
                                         b, hq, hkv, d, n_slots, max_len, 0.088, out.data_ptr(), 1, None) == 0
+        case(f"decode_attention_quant {hq}/{hkv}")
+        lens2 = torch.tensor([2, 40, 0], dtype=torch.int32)        # an invalid sequence too
+        out2 = torch.empty(b, hq, d, dtype=torch.bfloat16)
+        xq = torch.empty(b, hq * d, dtype=torch.int8)
+        xs = torch.empty(b)
+        cnt = torch.zeros(b, dtype=torch.int32)
+        assert lib.tvq_decode_attention_quant(q.data_ptr(), q.stride(0), kn.data_ptr(), kn.stride(0), vn.data_ptr(),
+                                              vn.stride(0), kc.data_ptr(), vc.data_ptr(), slots.data_ptr(),
+                                              lens2.data_ptr(), b, hq, hkv, d, n_slots, max_len, 0.088,
+                                              out2.data_ptr(), 1, xq.data_ptr(), xs.data_ptr(), 1e-8,
+                                              cnt.data_ptr(), cnt.numel(), None) == 0
+        rq, rs = oracle.c_act_quant(bits16(out2.view(b, -1)))
+        assert np.array_equal(xq.numpy(), rq) and np.array_equal(xs.numpy(), rs) and int(cnt.abs().sum()) == 0
     case("qk_norm_rope")
     t, hq, hkv, max_pos = 5, 4, 2, 64
     qkv = torch.randn(t, (hq + 2 * hkv) * d).to(torch.bfloat16)

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(hiplib):
 
 
 def test_abi_version_and_errors_without_gpu(hiplib):
-    assert hiplib.tvq_abi_version() == 4
+    assert hiplib.tvq_abi_version() == 5
     assert hiplib.tvq_gemm_workspace_bytes() >= 16 << 20
     assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None, 0, None) == -1
     assert b"dtype" in hiplib.tvq_last_error()
@@ -71,6 +71,20 @@ def test_abi_version_and_errors_without_gpu(hiplib):
     assert b"K % 128" in hiplib.tvq_last_error()
     assert hiplib.tvq_gemm_operand_floor(1, 0x1008, 0x1000, 4, 8, 128, None) == -2
     assert hiplib.tvq_gemm_operand_floor(2, None, 0x1000, 4, 8, 128, None) == -1
+    # attention with the fused o_proj quantization: its own arguments are checked first
+    assert hiplib.tvq_prefill_attention_quant(None, None, None, 0, None, 2, 16, 8, 128, 0.1, None, 1, None, None,
+                                              1e-8, None, 0, None) == -1
+    assert b"null xq" in hiplib.tvq_last_error()
+    assert hiplib.tvq_prefill_attention_quant(None, None, None, 0, None, 2, 16, 8, 128, 0.1, None, 1, 0x1000,
+                                              0x1000, 1e-8, 0x1000, 1, None) == -1
+    assert b"counters hold 1" in hiplib.tvq_last_error()
+    assert hiplib.tvq_decode_attention_quant(None, 0, None, 0, None, 0, None, None, None, None, 3, 16, 8, 128, 4,
+                                             64, 0.1, None, 1, 0x1000, 0x1000, 0.0, 0x1000, 8, None) == -1
+    assert b"eps" in hiplib.tvq_last_error()
+    assert hiplib.tvq_decode_attention_quant(None, 0, None, 0, None, 0, None, None, None, None, 3, 16, 8, 128, 4,
+                                             64, 0.1, None, 1, 0x1001, 0x1000, 1e-8, 0x1000, 8, None) == -2
+    assert hiplib.tvq_decode_attention_quant(None, 0, None, 0, None, 0, None, None, None, None, 0, 16, 8, 128, 4,
+                                             64, 0.1, None, 1, None, None, 1e-8, None, 0, None) == 0
     assert hiplib.tvq_rmsnorm(None, None, None, 1e-6, None, None, None, 1, 4, 16, None) == -1
     assert b"null pointer" in hiplib.tvq_last_error()
     assert hiplib.tvq_rmsnorm(1, None, 1, 1e-6, None, None, None, 1, 4, 16, None) == -1

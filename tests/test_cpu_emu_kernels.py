@@ -566,6 +566,98 @@ def test_prefill_attention(hip, elib, hq, hkv):
     assert ((out.float() - ref).norm() / ref.norm()).item() < 8e-3
 
 
+# ---------------------------------------------------------------- attention with o_proj's quantization fused
+
+def _counters(n=64):
+    return torch.zeros(n, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2)])
+def test_prefill_attention_quant(hip, elib, hq, hkv, dtype):
+    """The quantizing prefill attention writes the same output as the plain
+    kernel, and int8 codes / scales bit-identical to act-quant of that
+    output; the counters are zero afterwards (two calls in a row, the second
+    smaller)."""
+    d = 128
+    for lens in ([1, 5, 64, 65, 129], [3, 70]):
+        t = sum(lens)
+        g = torch.Generator().manual_seed(hq + hkv + t)
+        q = torch.randn(t, hq, d, generator=g).to(dtype)
+        k = torch.randn(t, hkv, d, generator=g).to(dtype)
+        qkv = torch.randn(t, (hq + 2 * hkv) * d, generator=g).to(dtype)
+        v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+        offs, o = [], 0
+        for n in lens:
+            offs.append((o, n))
+            o += n
+        blocks = hip.prefill_blocks(offs)
+        dt = hip._TORCH_TO_TVQ[dtype]
+        ref = torch.empty_like(q)
+        assert elib.tvq_prefill_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0), blocks.data_ptr(),
+                                          blocks.shape[0], hq, hkv, d, d ** -0.5, ref.data_ptr(), dt, None) == 0
+        out = torch.empty_like(q)
+        xq = torch.full((t, hq * d), 77, dtype=torch.int8)
+        xs = torch.full((t,), -1.0)
+        cnt = _counters()
+        rc = elib.tvq_prefill_attention_quant(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0),
+                                              blocks.data_ptr(), blocks.shape[0], hq, hkv, d, d ** -0.5,
+                                              out.data_ptr(), dt, xq.data_ptr(), xs.data_ptr(), 1e-8,
+                                              cnt.data_ptr(), cnt.numel(), None)
+        assert rc == 0, elib.tvq_last_error()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        rq, rs = oracle.c_act_quant(bits16(ref.view(t, -1)), is_bf16=dtype == torch.bfloat16)
+        np.testing.assert_array_equal(xq.numpy(), rq)
+        np.testing.assert_array_equal(xs.numpy().view(np.uint32), rs.view(np.uint32))
+        assert int(cnt.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4)])
+def test_decode_attention_quant(elib, hq, hkv, dtype):
+    """The quantizing decode attention: same output and cache update as the
+    plain kernel, codes and scales bit-identical to act-quant of the output,
+    an invalid sequence's row quantized from its zero output, counters zero
+    afterwards."""
+    g = torch.Generator().manual_seed(hq * 3 + hkv)
+    n_slots, max_len, d = 5, 80, 128
+    kc0 = torch.randn(n_slots, hkv, max_len, d, generator=g).to(dtype)
+    vc0 = torch.randn(n_slots, hkv, max_len, d, generator=g).to(dtype)
+    lens_l, slots_l = [1, 2, 17, 33, 80, 0], [3, 0, 4, 1, 2, 1]   # the last sequence is invalid (length 0)
+    b = len(lens_l)
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, generator=g).to(dtype)
+    q = qkv[:, : hq * d].view(b, hq, d)
+    k = qkv[:, hq * d: (hq + hkv) * d].view(b, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+    slots = torch.tensor(slots_l, dtype=torch.int32)
+    lens = torch.tensor(lens_l, dtype=torch.int32)
+    dt = 1 if dtype == torch.bfloat16 else 0
+    outs = []
+    for quant in (False, True):
+        kc, vc = kc0.clone(), vc0.clone()
+        out = torch.empty(b, hq, d, dtype=dtype)
+        args = (q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), kc.data_ptr(),
+                vc.data_ptr(), slots.data_ptr(), lens.data_ptr(), b, hq, hkv, d, n_slots, max_len, d ** -0.5,
+                out.data_ptr(), dt)
+        if quant:
+            xq = torch.full((b, hq * d), 5, dtype=torch.int8)
+            xs = torch.full((b,), -1.0)
+            cnt = _counters()
+            rc = elib.tvq_decode_attention_quant(*args, xq.data_ptr(), xs.data_ptr(), 1e-8, cnt.data_ptr(),
+                                                 cnt.numel(), None)
+        else:
+            rc = elib.tvq_decode_attention(*args, None)
+        assert rc == 0, elib.tvq_last_error()
+        outs.append((out, kc, vc))
+    (o0, k0, v0), (o1, k1, v1) = outs
+    assert torch.equal(o0.view(torch.int16), o1.view(torch.int16))
+    assert torch.equal(k0, k1) and torch.equal(v0, v1)
+    rq, rs = oracle.c_act_quant(bits16(o0.view(b, -1)), is_bf16=dtype == torch.bfloat16)
+    np.testing.assert_array_equal(xq.numpy(), rq)
+    np.testing.assert_array_equal(xs.numpy().view(np.uint32), rs.view(np.uint32))
+    assert int(cnt.abs().sum()) == 0
+
+
 # ---------------------------------------------------------------- child-process modes
 
 def test_kernels_in_child_modes():

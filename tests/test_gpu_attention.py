@@ -143,3 +143,107 @@ def test_prefill_attention_matches_fp32_reference(hiplib, hq, hkv, dtype):
     tol = (1.5e-2 if dtype == torch.bfloat16 else 4e-3) * ref.abs().amax() + 1e-3
     assert err.max().item() <= tol, (err.max().item(), tol)
     assert ((out.float() - ref).norm() / ref.norm()).item() < (8e-3 if dtype == torch.bfloat16 else 2e-3)
+
+
+# ---------------------------------------------------------------- o_proj's quantization fused
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8), (24, 4), (6, 2)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_attention_quant_matches_plain_and_act_quant(hiplib, hq, hkv, dtype):
+    """tvq_prefill_attention_quant: the same output as tvq_prefill_attention,
+    int8 codes and scales bit-identical to tvq_act_quant of that output (and
+    to the oracle), counters zero afterwards; two calls in a row, the second
+    smaller."""
+    import numpy as np
+
+    import oracle
+    from nanovllm.quantization import _hip
+    d = 128
+    for lens in ([1, 5, 64, 65, 100, 300, 1024, 17, 128, 129, 255], [3, 70]):
+        print(f"CASE prefill_attention_quant hq={hq} hkv={hkv} dtype={dtype} lens={lens}", flush=True)
+        t = sum(lens)
+        g = torch.Generator(device="cuda").manual_seed(hq + hkv + t)
+        q = torch.randn(t, hq, d, device="cuda", generator=g).to(dtype)
+        k = torch.randn(t, hkv, d, device="cuda", generator=g).to(dtype)
+        qkv = torch.randn(t, (hq + 2 * hkv) * d, device="cuda", generator=g).to(dtype)
+        v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+        offs, o = [], 0
+        for n in lens:
+            offs.append((o, n))
+            o += n
+        blocks = _hip.prefill_blocks(offs).cuda()
+        ref = _hip.prefill_attention(q, k, v, blocks, d ** -0.5)
+        out, xq, xs = _hip.prefill_attention_quant(q, k, v, blocks, d ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        rq, rs = _hip.act_quant(ref.view(t, -1))
+        assert torch.equal(xq, rq) and torch.equal(xs.view(torch.int32), rs.view(torch.int32))
+        oq, os_ = oracle.c_act_quant(ref.view(t, -1).cpu().view(torch.int16).numpy().view(np.uint16),
+                                     is_bf16=dtype == torch.bfloat16)
+        np.testing.assert_array_equal(xq.cpu().numpy(), oq)
+        assert int(_hip.attn_counters(torch.device("cuda", 0)).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
+def test_decode_attention_quant_matches_plain_and_act_quant(hiplib, hq, hkv):
+    from nanovllm.quantization import _hip
+    print(f"CASE decode_attention_quant hq={hq} hkv={hkv}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(hq + 7 * hkv)
+    n_slots, max_len, d, dtype = 12, 1100, 128, torch.bfloat16
+    kc0 = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).to(dtype)
+    vc0 = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).to(dtype)
+    lens_l = [1, 2, 17, 16, 33, 100, 1000, 1100, 257, 0]   # the last sequence is invalid
+    slots_l = [3, 0, 11, 5, 7, 1, 2, 9, 10, 4]
+    b = len(lens_l)
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, device="cuda", generator=g).to(dtype)
+    q = qkv[:, : hq * d].view(b, hq, d)
+    k = qkv[:, hq * d: (hq + hkv) * d].view(b, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+    slots = torch.tensor(slots_l, dtype=torch.int32, device="cuda")
+    lens = torch.tensor(lens_l, dtype=torch.int32, device="cuda")
+    kc, vc = kc0.clone(), vc0.clone()
+    ref = _hip.decode_attention(q, k, v, kc, vc, slots, lens, d ** -0.5)
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    out, xq, xs = _hip.decode_attention_quant(q, k, v, kc2, vc2, slots, lens, d ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    rq, rs = _hip.act_quant(ref.view(b, -1))
+    assert torch.equal(xq, rq) and torch.equal(xs.view(torch.int32), rs.view(torch.int32))
+    assert int(_hip.attn_counters(torch.device("cuda", 0)).abs().sum()) == 0
+
+
+def test_decode_attention_quant_in_graph_replays(hiplib):
+    """Captured with its counters allocated beforehand, the quantizing decode
+    attention replays with new lengths exactly as eager calls do."""
+    from nanovllm.quantization import _hip
+    print("CASE decode_attention_quant graph", flush=True)
+    hq, hkv, d, n_slots, max_len = 16, 8, 128, 4, 512
+    g = torch.Generator(device="cuda").manual_seed(11)
+    kc = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_slots, hkv, max_len, d, device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn(4, hq, d, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(4, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(4, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+    slots = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([5, 9, 100, 1], dtype=torch.int32, device="cuda")
+    _hip.attn_counters(torch.device("cuda", 0))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _hip.decode_attention_quant(q, k, v, kc.clone(), vc.clone(), slots, lens, 0.088)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    kg, vg = kc.clone(), vc.clone()
+    with torch.cuda.graph(graph):
+        got = _hip.decode_attention_quant(q, k, v, kg, vg, slots, lens, 0.088)
+    for new_lens in ([5, 9, 100, 1], [300, 2, 7, 512], [1, 1, 1, 1]):
+        lens.copy_(torch.tensor(new_lens, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _hip.decode_attention_quant(q, k, v, kg.clone(), vg.clone(), slots, lens, 0.088)
+        torch.cuda.synchronize()
+        for a, b in zip(got, ref):
+            assert torch.equal(a.view(torch.uint8) if a.dtype != torch.int8 else a,
+                               b.view(torch.uint8) if b.dtype != torch.int8 else b)
+

@@ -59,9 +59,10 @@ def _rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
 @pytest.mark.parametrize("mode", ["int8", "w8a8"])
 def test_quantized_projections_run_native(gpu, hiplib, monkeypatch, mode):
     calls = {"n": 0}
-    # W8A16: every projection is one tvq_w8a16_gemm. W8A8: o_proj quantizes its
-    # input itself (tvq_w8a8_linear); qkv / gate_up / down receive int8 codes
-    # from the fused norm / SiLU producers (tvq_w8a8_gemm).
+    # W8A16: every projection is one tvq_w8a16_gemm. W8A8: every projection
+    # receives int8 codes from a producer with the quantization fused in
+    # (qkv / gate_up / down from the norm and SiLU kernels, o_proj from the
+    # attention kernel) and runs tvq_w8a8_gemm.
     names = ["w8a16_gemm"] if mode == "int8" else ["w8a8_linear", "w8a8_gemm"]
 
     def counting(orig):
@@ -128,7 +129,7 @@ def _check_projections_against_oracle(llm, mode, arch, prompt):
             assert oracle.max_abs_ratio(yf, rf) <= oracle.MAX_ABS_TOL
         # against its own numerics the kernel is far tighter than the tolerance
         assert oracle.rel_l2(yf, ref_own.float().numpy()) < 2e-3
-    assert fused == (3 * layers if mode == "w8a8" else 0)
+    assert fused == (4 * layers if mode == "w8a8" else 0)  # o_proj's codes come from the attention kernel
 
 
 @pytest.mark.parametrize("mode", ["int8", "w8a8"])

@@ -369,4 +369,68 @@ int tvq_prefill_attention(const void* q, const void* k, const void* v, int64_t v
   return ok();
 }
 
+namespace {
+
+// Checks of the quantized-output arguments of the attention entry points.
+int check_attn_quant(int8_t* xq, float* a_scales, int32_t* counters, int64_t counters_len, int64_t needed,
+                     float eps) {
+  if (!xq || !a_scales || !counters) return fail(TVQ_E_INVALID, "null xq / a_scales / counters");
+  if (counters_len < needed)
+    return fail(TVQ_E_INVALID, "counters hold %lld entries, %lld needed", (long long)counters_len, (long long)needed);
+  if (((uintptr_t)xq & 3u) != 0 || ((uintptr_t)counters & 3u) != 0)
+    return fail(TVQ_E_UNSUPPORTED, "xq and counters must be 4-byte aligned");
+  if (!(eps > 0.0f)) return fail(TVQ_E_INVALID, "eps must be positive");
+  return TVQ_OK;
+}
+
+}  // namespace
+
+int tvq_decode_attention_quant(const void* q, int64_t q_stride, const void* k_new, int64_t k_stride,
+                               const void* v_new, int64_t v_stride, void* k_cache, void* v_cache,
+                               const int32_t* slots, const int32_t* lens, int64_t B, int Hq, int Hkv, int head_dim,
+                               int64_t num_slots, int64_t max_len, float scale, void* out, int dtype, int8_t* xq,
+                               float* a_scales, float eps, int32_t* counters, int64_t counters_len, void* stream) {
+  if (B > 0)
+    if (int rc = check_attn_quant(xq, a_scales, counters, counters_len, B, eps)) return rc;
+  if (int rc = check_dtype(dtype)) return rc;
+  if (B < 0 || B > kMaxDim || max_len <= 0 || max_len > kMaxDim || num_slots <= 0 || num_slots > kMaxDim)
+    return fail(TVQ_E_INVALID, "invalid B / num_slots / max_len");
+  if (B == 0) return ok();
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !slots || !lens || !out)
+    return fail(TVQ_E_INVALID, "null pointer argument");
+  if (head_dim != 128) return fail(TVQ_E_UNSUPPORTED, "head_dim must be 128, got %d", head_dim);
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || (Hq / Hkv != 1 && Hq / Hkv != 2 && Hq / Hkv != 4))
+    return fail(TVQ_E_UNSUPPORTED, "Hq/Hkv must be 1, 2 or 4 (Hq=%d, Hkv=%d)", Hq, Hkv);
+  if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(k_cache) || !aligned16(v_cache) ||
+      !aligned16(out) || q_stride % 8 || k_stride % 8 || v_stride % 8)
+    return fail(TVQ_E_UNSUPPORTED, "decode attention needs 16-byte aligned pointers and strides");
+  const AttnQuant qo{xq, a_scales, counters, eps};
+  hipError_t e = launch_decode_attention(q, q_stride, k_new, k_stride, v_new, v_stride, k_cache, v_cache, slots, lens,
+                                         (int)B, Hq, Hkv, (int)max_len, (int)num_slots, scale, out,
+                                         dtype == TVQ_DTYPE_BF16, (hipStream_t)stream, &qo);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "decode attention launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int tvq_prefill_attention_quant(const void* q, const void* k, const void* v, int64_t v_stride, const int32_t* blocks,
+                                int64_t nblocks, int Hq, int Hkv, int head_dim, float scale, void* out, int dtype,
+                                int8_t* xq, float* a_scales, float eps, int32_t* counters, int64_t counters_len,
+                                void* stream) {
+  if (nblocks > 0)
+    if (int rc = check_attn_quant(xq, a_scales, counters, counters_len, nblocks, eps)) return rc;
+  if (int rc = check_dtype(dtype)) return rc;
+  if (nblocks < 0 || nblocks > kMaxDim) return fail(TVQ_E_INVALID, "invalid nblocks");
+  if (nblocks == 0) return ok();
+  if (!q || !k || !v || !blocks || !out) return fail(TVQ_E_INVALID, "null pointer argument");
+  if (head_dim != 128) return fail(TVQ_E_UNSUPPORTED, "head_dim must be 128, got %d", head_dim);
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || Hq > 65535) return fail(TVQ_E_INVALID, "invalid Hq / Hkv");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || v_stride % 8)
+    return fail(TVQ_E_UNSUPPORTED, "prefill attention needs 16-byte aligned pointers and strides");
+  const AttnQuant qo{xq, a_scales, counters, eps};
+  hipError_t e = launch_prefill_attention(q, k, v, v_stride, blocks, (int)nblocks, Hq, Hkv, scale, out,
+                                          dtype == TVQ_DTYPE_BF16, (hipStream_t)stream, &qo);
+  if (e != hipSuccess) return fail(TVQ_E_HIP, "prefill attention launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -43,14 +43,96 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
   }
 }
 
-template <typename T, int G>
+// ---- o_proj's per-token quantization, fused (W8A8) ----------------------
+// A token's attention output row [Hq * 128] is produced by several
+// workgroups (one per kv head or head group). In the quantizing variants
+// every workgroup stores its slice with agent-scope stores, which go through
+// the XCD's L2 to the device-coherent level, waits for them, and counts
+// itself in its row block's counter with an agent-scope atomic; the last of
+// the block's workgroups reads the rows back with agent-scope loads (past
+// any stale L2 line) and writes their int8 codes and scales exactly as
+// tvq_act_quant does (s = max(RN(amax / 127), eps), the divide-free code),
+// then zeroes the counter. No workgroup waits on another, and the codes are
+// bit-identical to quantizing the stored output with tvq_act_quant.
+
+// Agent-scope 8-byte store of four 16-bit outputs.
+__device__ __forceinline__ void store8_agent(uint16_t* p, u32x2 v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ float absmax4(uint64_t w) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(to_float<T>((uint16_t)(w >> (16 * i)))));
+  return m;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t codes4(uint64_t w, float s, float rs) {
+  uint32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c |= ((uint32_t)(int32_t)quant_code(to_float<T>((uint16_t)(w >> (16 * i))), s, rs) & 0xffu)
+                                   << (8 * i);
+  return c;
+}
+
+// The handoff and, in the last arriving workgroup, the quantization of rows
+// [r0, r1) of the [*, W] output (W % 4 == 0). Called by every thread of the
+// workgroup after its output stores.
+template <typename T, int kThreads>
+__device__ void quantize_rows_last(const uint16_t* out, int64_t r0, int64_t r1, int W, int32_t* cnt, int arrivals,
+                                   int8_t* xq, float* xs, float eps) {
+  __shared__ int last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's output stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == arrivals - 1;
+  __syncthreads();
+  if (!last) return;
+  constexpr int kWaves = kThreads / 64;
+  constexpr int kCache = 8;  // 8-byte vectors per lane kept in registers: rows up to 2048 wide are read once
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nv = W / 4;
+  for (int64_t row = r0 + wave; row < r1; row += kWaves) {
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(out + row * W);
+    uint64_t c[kCache];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCache; ++i) {
+      const int v = lane + 64 * i;
+      c[i] = v < nv ? __hip_atomic_load(src + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+      amax = fmaxf(amax, absmax4<T>(c[i]));
+    }
+    for (int v = lane + 64 * kCache; v < nv; v += 64)
+      amax = fmaxf(amax, absmax4<T>(__hip_atomic_load(src + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+    const float s = fmaxf(__fdiv_rn(amax, 127.0f), eps);
+    const float rs = __fdiv_rn(1.0f, s);
+    if (lane == 0) xs[row] = s;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + row * W);
+#pragma unroll
+    for (int i = 0; i < kCache; ++i) {
+      const int v = lane + 64 * i;
+      if (v < nv) dst[v] = codes4<T>(c[i], s, rs);
+    }
+    for (int v = lane + 64 * kCache; v < nv; v += 64)
+      dst[v] = codes4<T>(__hip_atomic_load(src + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), s, rs);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T, int G, bool kQ = false>
 __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __restrict__ q, int64_t q_stride,
                                                           const uint16_t* __restrict__ k_new, int64_t k_stride,
                                                           const uint16_t* __restrict__ v_new, int64_t v_stride,
                                                           uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
                                                           const int32_t* __restrict__ slots,
                                                           const int32_t* __restrict__ lens, int Hkv, int max_len,
-                                                          int num_slots, float scale, uint16_t* __restrict__ out) {
+                                                          int num_slots, float scale, uint16_t* __restrict__ out,
+                                                          AttnQuant qo) {
   const int b = blockIdx.x;
   const int g = blockIdx.y;
   const int tid = threadIdx.x;
@@ -60,7 +142,12 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
   const int64_t slot = slots[b];
   if (len < 1 || len > max_len || slot < 0 || slot >= num_slots) {
     // Invalid metadata: touch no cache memory, emit zeros (uniform per workgroup).
-    for (int e = tid; e < G * kD; e += 256) out[((int64_t)b * Hkv * G + g * G) * kD + e] = 0;
+    if constexpr (kQ) {
+      for (int e = 4 * tid; e < G * kD; e += 4 * 256) store8_agent(out + ((int64_t)b * Hkv * G + g * G) * kD + e, u32x2{0, 0});
+      quantize_rows_last<T, 256>(out, b, b + 1, Hkv * G * kD, qo.counters + b, Hkv, qo.xq, qo.a_scales, qo.eps);
+    } else {
+      for (int e = tid; e < G * kD; e += 256) out[((int64_t)b * Hkv * G + g * G) * kD + e] = 0;
+    }
     return;
   }
   const int64_t head_off = (slot * Hkv + g) * (int64_t)max_len * kD;
@@ -172,27 +259,50 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
     for (int i = 0; i < 8; ++i) so[grp][h][8 * li + i] = o[h][i];
   }
   __syncthreads();
-  for (int e = tid; e < G * kD; e += 256) {
-    const int h = e / kD;
-    const int d = e % kD;
-    float M = -INFINITY;
+  if constexpr (kQ) {
+    // four consecutive dims per thread, one agent-scope 8-byte store
+    for (int e = 4 * tid; e < G * kD; e += 4 * 256) {
+      const int h = e / kD;
+      float M = -INFINITY;
 #pragma unroll
-    for (int x = 0; x < kGroups; ++x) M = fmaxf(M, sm[x][h][0]);
-    float L = 0.0f, acc = 0.0f;
+      for (int x = 0; x < kGroups; ++x) M = fmaxf(M, sm[x][h][0]);
+      float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int x = 0; x < kGroups; ++x) {
-      const float w = sm[x][h][1] > 0.0f ? __builtin_amdgcn_exp2f(sm[x][h][0] - M) : 0.0f;
-      L = fmaf(sm[x][h][1], w, L);
-      acc = fmaf(so[x][h][d], w, acc);
+      for (int x = 0; x < kGroups; ++x) {
+        const float w = sm[x][h][1] > 0.0f ? __builtin_amdgcn_exp2f(sm[x][h][0] - M) : 0.0f;
+        L = fmaf(sm[x][h][1], w, L);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = fmaf(so[x][h][e % kD + t], w, acc[t]);
+      }
+      u32x2 pk;
+      pk.x = (uint32_t)from_float<T>(acc[0] / L) | ((uint32_t)from_float<T>(acc[1] / L) << 16);
+      pk.y = (uint32_t)from_float<T>(acc[2] / L) | ((uint32_t)from_float<T>(acc[3] / L) << 16);
+      store8_agent(out + ((int64_t)b * Hkv * G + g * G) * kD + e, pk);
     }
-    out[((int64_t)b * Hkv * G + g * G + h) * kD + d] = from_float<T>(acc / L);
+    quantize_rows_last<T, 256>(out, b, b + 1, Hkv * G * kD, qo.counters + b, Hkv, qo.xq, qo.a_scales, qo.eps);
+  } else {
+    for (int e = tid; e < G * kD; e += 256) {
+      const int h = e / kD;
+      const int d = e % kD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int x = 0; x < kGroups; ++x) M = fmaxf(M, sm[x][h][0]);
+      float L = 0.0f, acc = 0.0f;
+#pragma unroll
+      for (int x = 0; x < kGroups; ++x) {
+        const float w = sm[x][h][1] > 0.0f ? __builtin_amdgcn_exp2f(sm[x][h][0] - M) : 0.0f;
+        L = fmaf(sm[x][h][1], w, L);
+        acc = fmaf(so[x][h][d], w, acc);
+      }
+      out[((int64_t)b * Hkv * G + g * G + h) * kD + d] = from_float<T>(acc / L);
+    }
   }
 }
 
-template <typename T>
+template <typename T, bool kQ>
 hipError_t launch_t(const void* q, int64_t qs, const void* kn, int64_t ks, const void* vn, int64_t vs, void* kc,
                     void* vc, const int32_t* slots, const int32_t* lens, int B, int Hq, int Hkv, int max_len,
-                    int num_slots, float scale, void* out, hipStream_t st) {
+                    int num_slots, float scale, void* out, AttnQuant qo, hipStream_t st) {
   const dim3 grid((unsigned)B, (unsigned)Hkv), block(256);
   auto Q = static_cast<const uint16_t*>(q);
   auto KN = static_cast<const uint16_t*>(kn);
@@ -201,9 +311,9 @@ hipError_t launch_t(const void* q, int64_t qs, const void* kn, int64_t ks, const
   auto VC = static_cast<uint16_t*>(vc);
   auto O = static_cast<uint16_t*>(out);
   switch (Hq / Hkv) {
-    case 1: decode_attn_kernel<T, 1><<<grid, block, 0, st>>>(Q, qs, KN, ks, VN, vs, KC, VC, slots, lens, Hkv, max_len, num_slots, scale, O); break;
-    case 2: decode_attn_kernel<T, 2><<<grid, block, 0, st>>>(Q, qs, KN, ks, VN, vs, KC, VC, slots, lens, Hkv, max_len, num_slots, scale, O); break;
-    case 4: decode_attn_kernel<T, 4><<<grid, block, 0, st>>>(Q, qs, KN, ks, VN, vs, KC, VC, slots, lens, Hkv, max_len, num_slots, scale, O); break;
+    case 1: decode_attn_kernel<T, 1, kQ><<<grid, block, 0, st>>>(Q, qs, KN, ks, VN, vs, KC, VC, slots, lens, Hkv, max_len, num_slots, scale, O, qo); break;
+    case 2: decode_attn_kernel<T, 2, kQ><<<grid, block, 0, st>>>(Q, qs, KN, ks, VN, vs, KC, VC, slots, lens, Hkv, max_len, num_slots, scale, O, qo); break;
+    case 4: decode_attn_kernel<T, 4, kQ><<<grid, block, 0, st>>>(Q, qs, KN, ks, VN, vs, KC, VC, slots, lens, Hkv, max_len, num_slots, scale, O, qo); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -214,11 +324,15 @@ hipError_t launch_t(const void* q, int64_t qs, const void* kn, int64_t ks, const
 hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* k_new, int64_t k_stride,
                                    const void* v_new, int64_t v_stride, void* k_cache, void* v_cache,
                                    const int32_t* slots, const int32_t* lens, int B, int Hq, int Hkv, int max_len,
-                                   int num_slots, float scale, void* out, bool bf16, hipStream_t stream) {
-  return bf16 ? launch_t<BF16>(q, q_stride, k_new, k_stride, v_new, v_stride, k_cache, v_cache, slots, lens, B, Hq,
-                               Hkv, max_len, num_slots, scale, out, stream)
-              : launch_t<F16>(q, q_stride, k_new, k_stride, v_new, v_stride, k_cache, v_cache, slots, lens, B, Hq, Hkv,
-                              max_len, num_slots, scale, out, stream);
+                                   int num_slots, float scale, void* out, bool bf16, hipStream_t stream,
+                                   const AttnQuant* quant) {
+  const AttnQuant qo = quant ? *quant : AttnQuant{nullptr, nullptr, nullptr, 0.0f};
+#define TVQ_DEC(TT, QQ)                                                                                              \
+  launch_t<TT, QQ>(q, q_stride, k_new, k_stride, v_new, v_stride, k_cache, v_cache, slots, lens, B, Hq, Hkv, max_len, \
+                   num_slots, scale, out, qo, stream)
+  if (quant) return bf16 ? TVQ_DEC(BF16, true) : TVQ_DEC(F16, true);
+  return bf16 ? TVQ_DEC(BF16, false) : TVQ_DEC(F16, false);
+#undef TVQ_DEC
 }
 
 
@@ -261,12 +375,13 @@ constexpr int kBlkK = 64;
 constexpr int kKStride = kD + 8;      // K tile row stride (elements): 16-row fragment reads hit distinct banks
 constexpr int kVStride = kD + 16;     // V tile row stride (elements): the 4 rows of a transposing read hit distinct banks
 
-template <typename T, int G>
+template <typename T, int G, bool kQ = false>
 __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* __restrict__ q,
                                                                const uint16_t* __restrict__ k,
                                                                const uint16_t* __restrict__ v, int64_t v_stride,
                                                                const int32_t* __restrict__ blocks, int Hq, int Hkv,
-                                                               float scale_log2, uint16_t* __restrict__ out) {
+                                                               float scale_log2, uint16_t* __restrict__ out,
+                                                               AttnQuant qo) {
   constexpr int kThreads = 256 * G;
   constexpr int kVec = kBlkK * kD / 8;                 // 16-byte vectors per K (or V) tile
   constexpr int kPer = kVec / kThreads;                // per thread
@@ -417,9 +532,15 @@ __global__ __launch_bounds__(256 * G) void prefill_attn_kernel(const uint16_t* _
       u32x2 pk;
       pk.x = (uint32_t)from_float<T>(o[dt][0] * inv) | ((uint32_t)from_float<T>(o[dt][1] * inv) << 16);
       pk.y = (uint32_t)from_float<T>(o[dt][2] * inv) | ((uint32_t)from_float<T>(o[dt][3] * inv) << 16);
-      *reinterpret_cast<u32x2*>(dst + 16 * dt + 4 * g) = pk;
+      if constexpr (kQ)
+        store8_agent(dst + 16 * dt + 4 * g, pk);
+      else
+        *reinterpret_cast<u32x2*>(dst + 16 * dt + 4 * g) = pk;
     }
   }
+  if constexpr (kQ)
+    quantize_rows_last<T, 256 * G>(out, seq0 + q0, seq0 + min(q0 + kBlkQ, len), Hq * kD, qo.counters + blockIdx.x,
+                                   gridDim.y, qo.xq, qo.a_scales, qo.eps);
 }
 
 // Two values rounded to the 16-bit type, packed low | high << 16 (bf16:
@@ -459,10 +580,11 @@ __device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
 // MFMAs of key blocks that lie wholly after its last query (the block's
 // other wave may still need them) and the mask arithmetic of blocks that lie
 // wholly before its first query.
-template <typename T, int G>
+template <typename T, int G, bool kQ = false>
 __global__ __launch_bounds__(2 * kBlkQ * G) __attribute__((amdgpu_waves_per_eu(2))) void prefill_attn32_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t v_stride,
-    const int32_t* __restrict__ blocks, int Hq, int Hkv, float scale_log2, uint16_t* __restrict__ out) {
+    const int32_t* __restrict__ blocks, int Hq, int Hkv, float scale_log2, uint16_t* __restrict__ out,
+    AttnQuant qo) {
   constexpr int kWph = kBlkQ / 32;                     // waves per head
   constexpr int kThreads = 64 * kWph * G;
   constexpr int kVec = kBlkK * kD / 8;                 // 16-byte vectors per K (or V) tile
@@ -637,14 +759,20 @@ __global__ __launch_bounds__(2 * kBlkQ * G) __attribute__((amdgpu_waves_per_eu(2
         u32x2 pk;
         pk.x = (uint32_t)from_float<T>(o[dt][4 * j] * inv) | ((uint32_t)from_float<T>(o[dt][4 * j + 1] * inv) << 16);
         pk.y = (uint32_t)from_float<T>(o[dt][4 * j + 2] * inv) | ((uint32_t)from_float<T>(o[dt][4 * j + 3] * inv) << 16);
-        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * j) = pk;
+        if constexpr (kQ)
+          store8_agent(dst + 32 * dt + 8 * j, pk);
+        else
+          *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * j) = pk;
       }
   }
+  if constexpr (kQ)
+    quantize_rows_last<T, 2 * kBlkQ * G>(out, seq0 + q0, seq0 + min(q0 + kBlkQ, len), Hq * kD,
+                                         qo.counters + blockIdx.x, gridDim.y, qo.xq, qo.a_scales, qo.eps);
 }
 
-template <typename T>
+template <typename T, bool kQ>
 hipError_t launch_prefill_t(const uint16_t* Q, const uint16_t* K, const uint16_t* V, int64_t v_stride,
-                            const int32_t* blocks, int nblocks, int Hq, int Hkv, float sl2, uint16_t* O,
+                            const int32_t* blocks, int nblocks, int Hq, int Hkv, float sl2, uint16_t* O, AttnQuant qo,
                             hipStream_t stream) {
   // G query heads per workgroup: the largest of 4, 2, 1 dividing the GQA
   // ratio Hq / Hkv, so the workgroup's heads share one kv head. G = 2 and 4
@@ -654,11 +782,11 @@ hipError_t launch_prefill_t(const uint16_t* Q, const uint16_t* K, const uint16_t
   const int G = ratio % 4 == 0 ? 4 : (ratio % 2 == 0 ? 2 : 1);
   const dim3 grid((unsigned)nblocks, (unsigned)(Hq / G));
   if (G == 4)
-    prefill_attn32_kernel<T, 4><<<grid, 8 * kBlkQ, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O);
+    prefill_attn32_kernel<T, 4, kQ><<<grid, 8 * kBlkQ, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O, qo);
   else if (G == 2)
-    prefill_attn32_kernel<T, 2><<<grid, 4 * kBlkQ, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O);
+    prefill_attn32_kernel<T, 2, kQ><<<grid, 4 * kBlkQ, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O, qo);
   else
-    prefill_attn_kernel<T, 1><<<grid, 256, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O);
+    prefill_attn_kernel<T, 1, kQ><<<grid, 256, 0, stream>>>(Q, K, V, v_stride, blocks, Hq, Hkv, sl2, O, qo);
   return hipGetLastError();
 }
 
@@ -666,14 +794,19 @@ hipError_t launch_prefill_t(const uint16_t* Q, const uint16_t* K, const uint16_t
 
 hipError_t launch_prefill_attention(const void* q, const void* k, const void* v, int64_t v_stride,
                                     const int32_t* blocks, int nblocks, int Hq, int Hkv, float scale, void* out,
-                                    bool bf16, hipStream_t stream) {
+                                    bool bf16, hipStream_t stream, const AttnQuant* quant) {
   const float sl2 = scale * 1.4426950408889634f;  // log2(e)
   auto Q = static_cast<const uint16_t*>(q);
   auto Kp = static_cast<const uint16_t*>(k);
   auto V = static_cast<const uint16_t*>(v);
   auto O = static_cast<uint16_t*>(out);
-  if (bf16) return launch_prefill_t<BF16>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, stream);
-  return launch_prefill_t<F16>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, stream);
+  const AttnQuant qo = quant ? *quant : AttnQuant{nullptr, nullptr, nullptr, 0.0f};
+  if (quant) {
+    if (bf16) return launch_prefill_t<BF16, true>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, qo, stream);
+    return launch_prefill_t<F16, true>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, qo, stream);
+  }
+  if (bf16) return launch_prefill_t<BF16, false>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, qo, stream);
+  return launch_prefill_t<F16, false>(Q, Kp, V, v_stride, blocks, nblocks, Hq, Hkv, sl2, O, qo, stream);
 }
 
 }  // namespace tvq

@@ -32,19 +32,30 @@ struct GemmArgs {
 };
 
 bool act_quant_vec_ok(const void* x, const void* xq, int64_t K);
+
+// Attention output quantized for the W8A8 o_proj in the same launch: per-token
+// int8 codes [T, Hq*128] and fp32 scales [T], and the row-block counters of
+// the last-arrival handoff (zero on entry, left zero).
+struct AttnQuant {
+  int8_t* xq;
+  float* a_scales;
+  int32_t* counters;
+  float eps;
+};
 hipError_t launch_rmsnorm(const void* x, void* residual, const void* weight, float eps, void* y, int8_t* xq,
                           float* a_scales, bool bf16, int64_t M, int64_t K, hipStream_t stream);
 hipError_t launch_decode_attention(const void* q, int64_t q_stride, const void* k_new, int64_t k_stride,
                                    const void* v_new, int64_t v_stride, void* k_cache, void* v_cache,
                                    const int32_t* slots, const int32_t* lens, int B, int Hq, int Hkv, int max_len,
-                                   int num_slots, float scale, void* out, bool bf16, hipStream_t stream);
+                                   int num_slots, float scale, void* out, bool bf16, hipStream_t stream,
+                                   const AttnQuant* quant = nullptr);
 hipError_t launch_qk_norm_rope(const void* qkv, int64_t row_stride, const int64_t* positions, const float* cos_t,
                                const float* sin_t, const void* q_weight, const void* k_weight, float eps, int64_t T_,
                                int Hq, int Hkv, int max_pos, void* q_out, void* k_out, void* k_cache, void* v_cache,
                                const int64_t* slots, int num_slots, int max_len, bool bf16, hipStream_t stream);
 hipError_t launch_prefill_attention(const void* q, const void* k, const void* v, int64_t v_stride,
                                     const int32_t* blocks, int nblocks, int Hq, int Hkv, float scale, void* out,
-                                    bool bf16, hipStream_t stream);
+                                    bool bf16, hipStream_t stream, const AttnQuant* quant = nullptr);
 hipError_t launch_silu_mul(const void* gate_up, void* y, int8_t* xq, float* a_scales, bool bf16, int64_t M,
                            int64_t I, hipStream_t stream);
 hipError_t launch_act_quant(const void* x, bool bf16, int64_t M, int64_t K, float eps, int8_t* xq, float* a_scales,

@@ -99,9 +99,11 @@ class ModelRunner:
             random_init_(self.model, config.seed, device=device)
         self.model.eval()
         if device == "cuda":
-            # the split-K GEMM workspace must exist before any graph capture
+            # the split-K GEMM workspace and the attention kernels' counters
+            # must exist before any graph capture
             from nanovllm.quantization import _hip
             _hip.gemm_workspace(torch.device("cuda", 0))
+            _hip.attn_counters(torch.device("cuda", 0))
             self._warmup_model()
         self._allocate_kv_cache()
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}

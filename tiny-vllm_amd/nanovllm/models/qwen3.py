@@ -80,18 +80,28 @@ class Attention(nn.Module):
         self.scale = head_dim ** -0.5
         self.k_cache = self.v_cache = None  # set by the engine
 
-    def _prefill_gpu(self, q, k, v, ctx) -> torch.Tensor:
+    def _prefill_gpu(self, q, k, v, ctx, quant: bool):
         """HIP varlen causal attention over the packed prompts. The prompt
         tokens' K/V were already stored into their cache slots by the fused
         q/k-norm + rotary kernel (Qwen3Attention.forward)."""
+        if quant:
+            return self._quantized(*_hip.prefill_attention_quant(q, k, v, ctx.attn_blocks, self.scale))
         return _hip.prefill_attention(q, k, v, ctx.attn_blocks, self.scale)
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    @staticmethod
+    def _quantized(out: torch.Tensor, xq: torch.Tensor, scales: torch.Tensor) -> QuantizedActivation:
+        return QuantizedActivation(xq, scales, out.dtype, tuple(xq.shape))
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, quant: bool = False):
+        """softmax(scale q K^T) V; with `quant` (W8A8 o_proj on the GPU), the
+        output comes back as o_proj's per-token int8 codes and scales,
+        quantized inside the attention kernel (bit-identical to quantizing
+        the bf16 output)."""
         ctx = get_context()
         group = self.num_heads // self.num_kv_heads
         if ctx.is_prefill:
             if q.is_cuda:
-                return self._prefill_gpu(q, k, v, ctx)
+                return self._prefill_gpu(q, k, v, ctx, quant)
             # Host path (CPU tests): one causal attention per sequence
             # (host-side cu_seqlens_q), after writing its keys/values to its
             # cache slot.
@@ -116,6 +126,9 @@ class Attention(nn.Module):
             # HIP kernel: appends k/v at position lens-1 of each slot and
             # attends over the valid prefix only; lengths are read on the
             # device (graph-capturable).
+            if quant:
+                return self._quantized(*_hip.decode_attention_quant(q, k, v, self.k_cache, self.v_cache, slots, lens,
+                                                                     self.scale))
             return _hip.decode_attention(q, k, v, self.k_cache, self.v_cache, slots, lens, self.scale)
         # Host path (CPU tests): the running batch owns cache slots inside
         # [kv_lo, kv_hi); attention runs over that slice of the cache up to the
@@ -156,6 +169,7 @@ class Qwen3Attention(nn.Module):
                                         quantization=quantization)
         self.rotary_emb = RotaryEmbedding(cfg.head_dim, cfg.max_position_embeddings, cfg.rope_theta)
         self.attn = Attention(self.num_heads, self.num_kv_heads, self.head_dim)
+        self.fuse_quant = quantization == "w8a8"
         self.qk_norm = not cfg.attention_bias
         if self.qk_norm:
             self.q_norm = RMSNorm(cfg.head_dim, cfg.rms_norm_eps)
@@ -183,6 +197,9 @@ class Qwen3Attention(nn.Module):
             if self.qk_norm:
                 q, k = self.q_norm(q), self.k_norm(k)
             q, k = self.rotary_emb(positions, q, k)
+        if self.fuse_quant and q.is_cuda and _get_w8a8_backend_preference() == "native":
+            # W8A8: o_proj's per-token quantization happens inside the attention kernel
+            return self.o_proj(self.attn(q, k, v, quant=True))
         o = self.attn(q, k, v)
         return self.o_proj(o.reshape(-1, self.q_size))
 

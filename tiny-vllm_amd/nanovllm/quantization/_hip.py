@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_NAME = "libtinyvllm_quant.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OP_ACT_QUANT = 0
 OP_W8A16 = 1
@@ -54,6 +54,11 @@ SYMBOLS = (
                                      _VP)),
     ("tvq_decode_attention", _INT, (_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _INT, _INT, _INT, _I64,
                                     _I64, ctypes.c_float, _VP, _INT, _VP)),
+    ("tvq_decode_attention_quant", _INT, (_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _I64, _INT, _INT, _INT,
+                                          _I64, _I64, ctypes.c_float, _VP, _INT, _VP, _VP, ctypes.c_float, _VP, _I64,
+                                          _VP)),
+    ("tvq_prefill_attention_quant", _INT, (_VP, _VP, _VP, _I64, _VP, _I64, _INT, _INT, _INT, ctypes.c_float, _VP, _INT,
+                                           _VP, _VP, ctypes.c_float, _VP, _I64, _VP)),
 )
 
 
@@ -154,6 +159,24 @@ def gemm_workspace(device: torch.device) -> torch.Tensor:
         ws = torch.zeros(load_library().tvq_gemm_workspace_bytes(), dtype=torch.uint8, device=device)
         _WORKSPACES[idx] = ws
     return ws
+
+
+_ATTN_COUNTERS: dict[int, torch.Tensor] = {}
+ATTN_COUNTERS = 1 << 16  # row blocks (prefill) or sequences (decode) per quantizing attention call
+
+
+def attn_counters(device: torch.device) -> torch.Tensor:
+    """The device's counters for the attention kernels' fused o_proj
+    quantization: zero-filled on first use, left zero by every call (calls
+    are ordered on the current stream). Allocate before HIP-graph capture."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    c = _ATTN_COUNTERS.get(idx)
+    if c is None:
+        _require(not torch.cuda.is_current_stream_capturing(),
+                 "the attention counters must be allocated before HIP-graph capture (call attn_counters(device))")
+        c = torch.zeros(ATTN_COUNTERS, dtype=torch.int32, device=device)
+        _ATTN_COUNTERS[idx] = c
+    return c
 
 
 def _ws(dev: torch.device, split_k: bool) -> tuple[int | None, int]:
@@ -519,3 +542,69 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, blocks:
                                        _TORCH_TO_TVQ[q.dtype], _stream(dev))
     _check(rc, "tvq_prefill_attention")
     return out
+
+
+def prefill_attention_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, blocks: torch.Tensor,
+                            scale: float, eps: float = 1e-8) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """prefill_attention, with o_proj's per-token int8 quantization of the
+    output in the same launch: returns (out, xq [T, Hq*D], a_scales [T]),
+    the codes bit-identical to act_quant(out.view(T, -1), eps)."""
+    lib = load_library()
+    dev = q.device
+    _require(q.is_cuda and q.is_contiguous() and k.is_contiguous(), "q and k must be contiguous GPU tensors")
+    _require(v.is_cuda and v.dim() == 3 and v.stride(2) == 1 and v.stride(1) == v.shape[2],
+             "v must be [T, Hkv, D] with contiguous heads")
+    _require(blocks.is_cuda and blocks.dtype == torch.int32 and blocks.is_contiguous() and blocks.dim() == 2,
+             "blocks must be a contiguous int32 [n, 3] GPU tensor")
+    _require(q.dtype in _TORCH_TO_TVQ and k.dtype == q.dtype and v.dtype == q.dtype, "dtype mismatch")
+    t, hq, d = q.shape
+    out = torch.empty_like(q)
+    xq = torch.empty((t, hq * d), dtype=torch.int8, device=dev)
+    a_s = torch.empty((t,), dtype=torch.float32, device=dev)
+    if blocks.shape[0] == 0:
+        return out, xq, a_s
+    cnt = attn_counters(dev)
+    with torch.cuda.device(dev):
+        rc = lib.tvq_prefill_attention_quant(q.data_ptr(), k.data_ptr(), v.data_ptr(), v.stride(0), blocks.data_ptr(),
+                                             blocks.shape[0], hq, k.shape[1], d, scale, out.data_ptr(),
+                                             _TORCH_TO_TVQ[q.dtype], xq.data_ptr(), a_s.data_ptr(), eps,
+                                             cnt.data_ptr(), cnt.numel(), _stream(dev))
+    _check(rc, "tvq_prefill_attention_quant")
+    return out, xq, a_s
+
+
+def decode_attention_quant(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                           v_cache: torch.Tensor, slots: torch.Tensor, lens: torch.Tensor, scale: float,
+                           eps: float = 1e-8, out: torch.Tensor | None = None
+                           ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """decode_attention, with o_proj's per-token int8 quantization of the
+    output in the same launch: returns (out, xq [B, Hq*D], a_scales [B])."""
+    lib = load_library()
+    dev = q.device
+    for t in (q, k_new, v_new):
+        _require(t.is_cuda and t.dim() == 3 and t.stride(2) == 1 and t.stride(1) == t.shape[2],
+                 "q / k_new / v_new must be [B, H, D] with contiguous heads")
+    for t in (k_cache, v_cache, slots, lens):
+        _require(t.is_cuda and t.is_contiguous(), "cache / slots / lens must be contiguous GPU tensors")
+    _require(slots.dtype == torch.int32 and lens.dtype == torch.int32, "slots and lens must be int32")
+    b, hq, d = q.shape
+    hkv = k_new.shape[1]
+    _require(k_cache.dim() == 4 and k_cache.shape[1] == hkv and k_cache.shape[3] == d and
+             v_cache.shape == k_cache.shape, "caches must be [slots, Hkv, max_len, D]")
+    _require(q.dtype in _TORCH_TO_TVQ and k_cache.dtype == q.dtype, "dtype mismatch")
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=dev)
+    xq = torch.empty((b, hq * d), dtype=torch.int8, device=dev)
+    a_s = torch.empty((b,), dtype=torch.float32, device=dev)
+    if b == 0:
+        return out, xq, a_s
+    cnt = attn_counters(dev)
+    with torch.cuda.device(dev):
+        rc = lib.tvq_decode_attention_quant(q.data_ptr(), q.stride(0), k_new.data_ptr(), k_new.stride(0),
+                                            v_new.data_ptr(), v_new.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+                                            slots.data_ptr(), lens.data_ptr(), b, hq, hkv, d, k_cache.shape[0],
+                                            k_cache.shape[2], scale, out.data_ptr(), _TORCH_TO_TVQ[q.dtype],
+                                            xq.data_ptr(), a_s.data_ptr(), eps, cnt.data_ptr(), cnt.numel(),
+                                            _stream(dev))
+    _check(rc, "tvq_decode_attention_quant")
+    return out, xq, a_s
