@@ -1,14 +1,16 @@
 """Build the kernel sources of tiny-vllm_amd/csrc for the CPU emulation
 (test infrastructure: hip/hip_runtime.h, emu_runtime.cpp).
 
-The sources are copied unchanged except for four mechanical rewrites that
+The sources are copied unchanged except for these mechanical rewrites, which
 host C++ cannot express:
   * kernel<<<grid, block, shmem, stream>>>(args)  ->  ::emu::launch(&kernel, grid, block, shmem, stream, args)
   * inline asm: "s_barrier" -> ::emu::barrier(); a vmcnt(N) wait ->
     ::emu::wait_vm(N); an LDS wait (lgkmcnt) -> ::emu::wave_barrier();
     register pins dropped
   * __attribute__((address_space(N))) and the amdgpu_* kernel attributes dropped
-  * extern __shared__ T name[]  ->  T* name = (T*)::emu::dyn_smem()
+  * extern __shared__ T name[]  ->  T* name = (T*)::emu::dyn_smem(), and a
+    static __shared__ T name[..] -> a reference to this workgroup's own
+    storage (::emu::lds), so concurrently resident workgroups do not share it
 and compiled with the host clang into tests/cpu_emu/_build/libtvq_emu[_asan].so,
 which exports the same C ABI as the product library (include/tvq.h).
 
@@ -127,6 +129,50 @@ def _rewrite_asm(src: str) -> str:
         pos = end
 
 
+def _split_top(text: str) -> list[str]:
+    parts, depth, cur = [], 0, ""
+    for c in text:
+        if c in "[(<":
+            depth += 1
+        elif c in "])>":
+            depth -= 1
+        if c == "," and depth == 0:
+            parts.append(cur)
+            cur = ""
+        else:
+            cur += c
+    parts.append(cur)
+    return [p.strip() for p in parts]
+
+
+def _rewrite_static_shared(src: str) -> str:
+    """`__shared__ [attrs] TYPE a[..], b;` -> references to per-workgroup
+    storage: `TYPE (&a)[..] = ::emu::lds<TYPE[..]>(key); TYPE (&b) = ...`."""
+    out, pos = [], 0
+    pat = re.compile(r"(?<!extern )\b__shared__\b")
+    while True:
+        m = pat.search(src, pos)
+        if not m:
+            out.append(src[pos:])
+            return "".join(out)
+        end = src.index(";", m.end())
+        body = re.sub(r"__attribute__\(\((?:[^()]|\([^()]*\))*\)\)", " ", src[m.end():end]).strip()
+        decls = _split_top(body)
+        first = re.match(r"(.*?)\b([A-Za-z_]\w*)\s*((?:\[[^\]]*\]\s*)*)$", decls[0], re.S)
+        assert first, decls[0]
+        ty = first.group(1).strip()
+        items = [(first.group(2), first.group(3).strip())]
+        for d in decls[1:]:
+            mm = re.match(r"([A-Za-z_]\w*)\s*((?:\[[^\]]*\]\s*)*)$", d, re.S)
+            assert mm, d
+            items.append((mm.group(1), mm.group(2).strip()))
+        key = "([] { static const char emu_tag = 0; return (const void*)&emu_tag; }())"
+        repl = " ".join(f"{ty} (&{name}){dims} = ::emu::lds<{ty}{dims}>({key});" for name, dims in items)
+        out.append(src[pos:m.start()])
+        out.append(repl)
+        pos = end + 1
+
+
 def rewrite(src: str) -> str:
     src = _rewrite_launches(src)
     src = _rewrite_asm(src)
@@ -134,6 +180,7 @@ def rewrite(src: str) -> str:
     src = re.sub(r"__attribute__\(\(amdgpu_\w+\((?:[^()]|\([^()]*\))*\)\)\)", "", src)
     src = re.sub(r"extern\s+__shared__\s+(?:__attribute__\(\(aligned\(\d+\)\)\)\s+)?(\w+)\s+(\w+)\[\]\s*;",
                  r"\1* \2 = reinterpret_cast<\1*>(::emu::dyn_smem());", src)
+    src = _rewrite_static_shared(src)
     return src
 
 

@@ -5,9 +5,11 @@ infrastructure), because the emulation's modes are fixed per process:
   --asan   the AddressSanitizer build, with the ASan runtime preloaded. Every
            buffer is a CPU tensor of exactly its size, so a read or write past
            any input, output, workspace or dynamic LDS allocation aborts.
-  (plain)  run with EMU_DMA=late (each LDS DMA lands only at its wave's
-           vmcnt wait) and EMU_SHUFFLE=seed (fibers in random order): a
-           missing DMA wait or a cross-wave race shows as a parity failure.
+  (plain)  run with EMU_CONCURRENT=32 (workgroups interleaved),
+           EMU_SHUFFLE=seed (random order, random stalls) and optionally
+           EMU_DMA=late (each LDS DMA lands only at its wave's vmcnt wait): a
+           missing DMA wait, a cross-wave race or an arrival-order assumption
+           between workgroups shows as a parity failure.
 
 Prints "all cases passed" at the end."""
 from __future__ import annotations

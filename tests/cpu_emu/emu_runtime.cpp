@@ -1,11 +1,20 @@
 // Fiber scheduler of the CPU emulation of HIP kernels (test infrastructure;
 // see hip/hip_runtime.h for the execution model).
+//
+// A launch runs its workgroups EMU_CONCURRENT at a time (default 1): the
+// fibers of all resident workgroups share one scheduler, so workgroups that
+// hand work to each other through global memory (split-K and stream-K
+// fixups, the attention kernels' fused quantization) meet in whatever order
+// the interleaving produces. Each resident workgroup has its own LDS: the
+// dynamic allocation and every static __shared__ array (see lds_slot).
 #include <stdio.h>
 #include <sys/mman.h>
 #include <ucontext.h>
 
+#include <algorithm>
 #include <deque>
 #include <random>
+#include <unordered_map>
 #include <vector>
 
 #include "hip/hip_runtime.h"
@@ -28,21 +37,13 @@ namespace {
 enum { kRun = 0, kWave = 1, kBar = 2, kDone = 3 };
 constexpr size_t kStack = 256 << 10;
 
+struct Block;
+
 struct Fiber {
   Lane lane;
   ucontext_t ctx;
   char* stack = nullptr;
-};
-
-struct Block {
-  dim3 bid, bdim, gdim;
-  int n = 0;
-  std::vector<Fiber>* fibers = nullptr;
-  const std::function<void()>* body = nullptr;
-  void* smem = nullptr;
-  ucontext_t sched;
-  const void* sched_stack_bottom = nullptr;
-  size_t sched_stack_size = 0;
+  Block* blk = nullptr;
 };
 
 struct DmaOp {
@@ -50,10 +51,28 @@ struct DmaOp {
   const char* src;
   int size;  // -1: the start of one wave instruction (one vm op)
 };
-std::vector<std::deque<DmaOp>> g_dma;  // per wave of the running workgroup
 
-void dma_flush_wave(int w, int keep_ops) {
-  std::deque<DmaOp>& q = g_dma[w];
+struct Block {
+  dim3 bid, bdim, gdim;
+  int n = 0;
+  Fiber* fibers = nullptr;
+  void* smem = nullptr;
+  std::unordered_map<const void*, void*> lds;  // static __shared__ arrays of this workgroup
+  std::vector<std::deque<DmaOp>> dma;          // per wave
+  bool active = false;
+};
+
+ucontext_t g_sched;
+const void* g_sched_stack_bottom = nullptr;
+size_t g_sched_stack_size = 0;
+Block* g_blk = nullptr;
+Fiber* g_cur = nullptr;
+const std::function<void()>* g_body = nullptr;
+hipError_t g_err = hipSuccess;
+std::vector<Fiber> g_pool;
+
+void dma_flush_wave(Block& b, int w, int keep_ops) {
+  std::deque<DmaOp>& q = b.dma[w];
   int ops = 0;
   for (const DmaOp& d : q) ops += d.size < 0;
   while (ops > keep_ops && !q.empty()) {
@@ -66,16 +85,11 @@ void dma_flush_wave(int w, int keep_ops) {
   }
 }
 
-Block* g_blk = nullptr;
-Fiber* g_cur = nullptr;
-hipError_t g_err = hipSuccess;
-std::vector<Fiber> g_pool;
-
 void to_sched() {
 #ifdef EMU_ASAN
-  __sanitizer_start_switch_fiber(nullptr, g_blk->sched_stack_bottom, g_blk->sched_stack_size);
+  __sanitizer_start_switch_fiber(nullptr, g_sched_stack_bottom, g_sched_stack_size);
 #endif
-  swapcontext(&g_cur->ctx, &g_blk->sched);
+  swapcontext(&g_cur->ctx, &g_sched);
 #ifdef EMU_ASAN
   __sanitizer_finish_switch_fiber(nullptr, nullptr, nullptr);
 #endif
@@ -83,21 +97,29 @@ void to_sched() {
 
 void fiber_entry() {
 #ifdef EMU_ASAN
-  __sanitizer_finish_switch_fiber(nullptr, &g_blk->sched_stack_bottom, &g_blk->sched_stack_size);
+  __sanitizer_finish_switch_fiber(nullptr, &g_sched_stack_bottom, &g_sched_stack_size);
 #endif
-  (*g_blk->body)();
+  (*g_body)();
   g_cur->lane.state = kDone;
 #ifdef EMU_ASAN
-  __sanitizer_start_switch_fiber(nullptr, g_blk->sched_stack_bottom, g_blk->sched_stack_size);
+  __sanitizer_start_switch_fiber(nullptr, g_sched_stack_bottom, g_sched_stack_size);
 #endif
-  setcontext(&g_blk->sched);
+  setcontext(&g_sched);
 }
 
-void run_block(Block& b) {
-  std::vector<Fiber>& F = *b.fibers;
+void start_block(Block& b, Fiber* fibers, dim3 bid, size_t shmem) {
+  b.bid = bid;
+  b.fibers = fibers;
+  b.active = true;
+  // dynamic shared memory: a fresh allocation of exactly the launch's size,
+  // filled with a NaN pattern (uninitialised LDS)
+  b.smem = shmem ? malloc(shmem) : nullptr;
+  if (shmem) memset(b.smem, 0xff, shmem);
+  b.dma.assign((b.n + 63) / 64, {});
   for (int i = 0; i < b.n; ++i) {
-    Fiber& f = F[i];
+    Fiber& f = fibers[i];
     const unsigned t = (unsigned)i;
+    f.blk = &b;
     f.lane.tid = dim3(t % b.bdim.x, (t / b.bdim.x) % b.bdim.y, t / (b.bdim.x * b.bdim.y));
     f.lane.wave = i / 64;
     f.lane.lane = i % 64;
@@ -109,72 +131,48 @@ void run_block(Block& b) {
     f.ctx.uc_link = nullptr;
     makecontext(&f.ctx, fiber_entry, 0);
   }
+}
+
+void finish_block(Block& b) {
+  for (size_t w = 0; w < b.dma.size(); ++w) dma_flush_wave(b, (int)w, 0);
+  free(b.smem);
+  b.smem = nullptr;
+  for (auto& kv : b.lds) free(kv.second);
+  b.lds.clear();
+  b.active = false;
+}
+
+// Resolve the wave-level operations of every wave of `b` whose waiting lanes
+// all wait on the same one; returns whether any ran.
+bool resolve_waves(Block& b) {
+  bool resolved = false;
   const int nwaves = (b.n + 63) / 64;
-  g_dma.assign(nwaves, {});
-  static const char* shuffle = getenv("EMU_SHUFFLE");
-  static std::mt19937 rng(shuffle ? (unsigned)atoi(shuffle) : 0u);
-  std::vector<int> order(b.n);
-  for (int i = 0; i < b.n; ++i) order[i] = i;
-  for (;;) {
-    bool ran = false;
-    if (shuffle) std::shuffle(order.begin(), order.end(), rng);
-    for (int oi = 0; oi < b.n; ++oi) {
-      const int i = order[oi];
-      if (F[i].lane.state != kRun) continue;
-      g_cur = &F[i];
-#ifdef EMU_ASAN
-      __sanitizer_start_switch_fiber(nullptr, F[i].stack, kStack);
-#endif
-      swapcontext(&b.sched, &F[i].ctx);
-#ifdef EMU_ASAN
-      __sanitizer_finish_switch_fiber(nullptr, nullptr, nullptr);
-#endif
-      g_cur = nullptr;
-      ran = true;
-    }
-    if (ran) continue;
-    // nothing runnable: resolve the wave-level operations first
-    bool resolved = false;
-    for (int w = 0; w < nwaves; ++w) {
-      Lane* L[64] = {};
-      WaveFn fn = nullptr;
-      bool any = false;
-      for (int l = 0; l < 64 && w * 64 + l < b.n; ++l) {
-        Lane& ln = F[w * 64 + l].lane;
-        if (ln.state != kWave) continue;
-        if (fn == nullptr) fn = ln.fn;
-        if (ln.fn != fn) {
-          fprintf(stderr, "emu: wave %d of block (%u,%u,%u): lanes wait on different wave operations\n", w, b.bid.x,
-                  b.bid.y, b.bid.z);
-          abort();
-        }
-        L[l] = &ln;
-        any = true;
+  for (int w = 0; w < nwaves; ++w) {
+    Lane* L[64] = {};
+    WaveFn fn = nullptr;
+    bool any = false;
+    for (int l = 0; l < 64 && w * 64 + l < b.n; ++l) {
+      Lane& ln = b.fibers[w * 64 + l].lane;
+      if (ln.state != kWave) continue;
+      if (fn == nullptr) fn = ln.fn;
+      if (ln.fn != fn) {
+        fprintf(stderr, "emu: wave %d of block (%u,%u,%u): lanes wait on different wave operations\n", w, b.bid.x,
+                b.bid.y, b.bid.z);
+        abort();
       }
-      if (!any) continue;
-      fn(L);
-      for (int l = 0; l < 64; ++l)
-        if (L[l]) L[l]->state = kRun;
-      resolved = true;
+      L[l] = &ln;
+      any = true;
     }
-    if (resolved) continue;
-    int live = 0, at_bar = 0;
-    for (int i = 0; i < b.n; ++i) {
-      if (F[i].lane.state != kDone) ++live;
-      if (F[i].lane.state == kBar) ++at_bar;
-    }
-    if (live == 0) {
-      for (int w = 0; w < nwaves; ++w) dma_flush_wave(w, 0);
-      break;
-    }
-    if (at_bar == live) {
-      for (int i = 0; i < b.n; ++i)
-        if (F[i].lane.state == kBar) F[i].lane.state = kRun;
-      continue;
-    }
-    fprintf(stderr, "emu: deadlock in block (%u,%u,%u)\n", b.bid.x, b.bid.y, b.bid.z);
-    abort();
+    if (!any) continue;
+    Block* saved = g_blk;
+    g_blk = &b;
+    fn(L);
+    g_blk = saved;
+    for (int l = 0; l < 64; ++l)
+      if (L[l]) L[l]->state = kRun;
+    resolved = true;
   }
+  return resolved;
 }
 
 }  // namespace
@@ -184,6 +182,15 @@ const dim3& block_idx() { return g_blk->bid; }
 const dim3& block_dim() { return g_blk->bdim; }
 const dim3& grid_dim() { return g_blk->gdim; }
 void* dyn_smem() { return g_blk->smem; }
+
+void* lds_slot(const void* key, size_t bytes) {
+  void*& p = g_blk->lds[key];
+  if (p == nullptr) {
+    p = aligned_alloc(1024, (bytes + 1023) / 1024 * 1024);
+    memset(p, 0xff, bytes);
+  }
+  return p;
+}
 
 int cu_count() {
   const char* e = getenv("EMU_CUS");
@@ -206,10 +213,12 @@ bool dma_late() {
   return e != nullptr && strcmp(e, "late") == 0;
 }
 
-void dma_enqueue(int wave, char* dst, const char* src, int size) { g_dma[wave].push_back(DmaOp{dst, src, size}); }
+void dma_enqueue(int wave, char* dst, const char* src, int size) {
+  g_blk->dma[wave].push_back(DmaOp{dst, src, size});
+}
 
 void wait_vm(int n) {
-  if (g_cur != nullptr && !g_dma.empty()) dma_flush_wave(g_cur->lane.wave, n);
+  if (g_cur != nullptr && !g_blk->dma.empty()) dma_flush_wave(*g_blk, g_cur->lane.wave, n);
 }
 
 void set_last_error(hipError_t e) { g_err = e; }
@@ -225,36 +234,99 @@ void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& 
     set_last_error(hipErrorInvalidConfiguration);
     return;
   }
-  if ((long)g_pool.size() < n) {
+  const long nblocks = (long)grid.x * grid.y * grid.z;
+  static const char* conc_env = getenv("EMU_CONCURRENT");
+  const int conc = (int)std::max(1L, std::min(nblocks, conc_env ? (long)atoi(conc_env) : 1L));
+  if ((long)g_pool.size() < n * conc) {
     const size_t old = g_pool.size();
-    g_pool.resize(n);
+    g_pool.resize(n * conc);
     for (size_t i = old; i < g_pool.size(); ++i) {
       void* s = mmap(nullptr, kStack, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
       if (s == MAP_FAILED) abort();
       g_pool[i].stack = static_cast<char*>(s);
     }
   }
-  Block b;
-  b.gdim = grid;
-  b.bdim = block;
-  b.n = (int)n;
-  b.fibers = &g_pool;
-  b.body = &body;
-  Block* saved = g_blk;
-  g_blk = &b;
-  for (unsigned z = 0; z < grid.z; ++z)
-    for (unsigned y = 0; y < grid.y; ++y)
-      for (unsigned x = 0; x < grid.x; ++x) {
-        b.bid = dim3(x, y, z);
-        // dynamic shared memory: a fresh allocation of exactly the launch's
-        // size per workgroup, filled with a NaN pattern (uninitialised LDS)
-        b.smem = shmem ? malloc(shmem) : nullptr;
-        if (shmem) memset(b.smem, 0xff, shmem);
-        run_block(b);
-        free(b.smem);
-        b.smem = nullptr;
-      }
-  g_blk = saved;
+  static const char* shuffle = getenv("EMU_SHUFFLE");
+  static std::mt19937 rng(shuffle ? (unsigned)atoi(shuffle) : 0u);
+  const std::function<void()>* saved_body = g_body;
+  g_body = &body;
+  std::vector<Block> slots(conc);
+  long next = 0;
+  auto bid_of = [&](long i) {
+    return dim3((unsigned)(i % grid.x), (unsigned)((i / grid.x) % grid.y), (unsigned)(i / ((long)grid.x * grid.y)));
+  };
+  for (int s = 0; s < conc; ++s) {
+    slots[s].bdim = block;
+    slots[s].gdim = grid;
+    slots[s].n = (int)n;
+    start_block(slots[s], &g_pool[s * n], bid_of(next++), shmem);
+  }
+  // One step of a resident workgroup: run its runnable fibers (each until it
+  // blocks); else resolve its waves' pending wave-level operations; else
+  // release its barrier, or retire it and start the next workgroup in its
+  // slot. Returns whether it progressed.
+  std::vector<Fiber*> order;
+  auto step = [&](int s) -> bool {
+    Block& b = slots[s];
+    order.clear();
+    for (int i = 0; i < b.n; ++i)
+      if (b.fibers[i].lane.state == kRun) order.push_back(&b.fibers[i]);
+    if (shuffle) std::shuffle(order.begin(), order.end(), rng);
+    for (Fiber* f : order) {
+      g_cur = f;
+      g_blk = f->blk;
+#ifdef EMU_ASAN
+      __sanitizer_start_switch_fiber(nullptr, f->stack, kStack);
+#endif
+      swapcontext(&g_sched, &f->ctx);
+#ifdef EMU_ASAN
+      __sanitizer_finish_switch_fiber(nullptr, nullptr, nullptr);
+#endif
+      g_cur = nullptr;
+    }
+    if (!order.empty()) return true;
+    if (resolve_waves(b)) return true;
+    int live = 0, at_bar = 0;
+    for (int i = 0; i < b.n; ++i) {
+      if (b.fibers[i].lane.state != kDone) ++live;
+      if (b.fibers[i].lane.state == kBar) ++at_bar;
+    }
+    if (live == 0) {
+      finish_block(b);
+      if (next < nblocks) start_block(b, &g_pool[s * n], bid_of(next++), shmem);
+      return true;
+    }
+    if (at_bar == live) {
+      for (int i = 0; i < b.n; ++i)
+        if (b.fibers[i].lane.state == kBar) b.fibers[i].lane.state = kRun;
+      return true;
+    }
+    return false;
+  };
+  std::vector<int> perm(conc);
+  for (int s = 0; s < conc; ++s) perm[s] = s;
+  for (;;) {
+    bool any_active = false, progress = false;
+    if (shuffle) std::shuffle(perm.begin(), perm.end(), rng);
+    for (int s : perm) {
+      if (!slots[s].active) continue;
+      any_active = true;
+      // shuffled mode: a resident workgroup sits out a step at random, so
+      // workgroups drift apart instead of moving in lockstep
+      if (shuffle && conc > 1 && (rng() & 1)) continue;
+      progress |= step(s);
+    }
+    if (!any_active) break;
+    if (progress) continue;
+    for (int s : perm)  // a step with nothing stalled
+      if (slots[s].active) progress |= step(s);
+    if (!progress) {
+      fprintf(stderr, "emu: deadlock (no workgroup can progress)\n");
+      abort();
+    }
+  }
+  g_body = saved_body;
+  g_blk = nullptr;
 }
 
 }  // namespace emu

@@ -4,15 +4,15 @@
 // and run on the CPU, under AddressSanitizer, against the oracle. The
 // product library is never built with it, and nothing in the package loads it.
 //
-// Execution model. A launch runs its workgroups one after another. Inside a
-// workgroup every work-item is a cooperative fiber (ucontext) on one OS
-// thread; a fiber runs until it reaches a workgroup barrier, a wave-level
+// Execution model. A launch runs its workgroups one after another, or
+// EMU_CONCURRENT=n of them interleaved. Every work-item is a cooperative
+// fiber (ucontext) on one OS thread; a fiber runs until it reaches a workgroup barrier, a wave-level
 // operation or its end. Wave-level operations (cross-lane shuffles,
 // readfirstlane, MFMA, the transposing LDS read, LDS DMA) are executed by the
 // scheduler for all lanes of the wave that wait on it, once no fiber can run:
-// lanes that have exited or sit elsewhere are the inactive lanes. Static
-// __shared__ arrays are function-local statics (one workgroup runs at a time),
-// dynamic shared memory is a fresh, poisoned allocation per workgroup.
+// lanes that have exited or sit elsewhere are the inactive lanes. Every
+// resident workgroup has its own LDS, static and dynamic, fresh and poisoned
+// (0xff) when the workgroup starts; EMU_CONCURRENT=n interleaves n workgroups.
 //
 // Arithmetic. MFMA results are computed in double and rounded once to fp32
 // (exact for the int8 forms); v_dot2 likewise. exp2 and rcp are the libm
@@ -21,7 +21,8 @@
 // With EMU_DMA=late it lands only at the wave's vmcnt wait (the latest).
 // An LDS wait (s_waitcnt lgkmcnt) is a rendezvous of the wave's lanes, which
 // stands in for the hardware's lockstep execution of a wave. EMU_SHUFFLE=seed
-// runs the fibers in a seeded random order instead of round-robin.
+// runs the fibers in a seeded random order instead of round-robin, and lets
+// interleaved workgroups sit out steps at random.
 #pragma once
 
 #include <math.h>
@@ -40,7 +41,6 @@
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
-#define __shared__ static
 #define __constant__
 #define __align__(n) __attribute__((aligned(n)))
 
@@ -85,6 +85,15 @@ const dim3& grid_dim();
 void barrier();
 void wave_sync(WaveFn fn);  // post this lane's inputs (in[]) and wait for the wave's result (out)
 void* dyn_smem();
+void* lds_slot(const void* key, size_t bytes);  // this workgroup's storage for one static __shared__ array
+
+// A static __shared__ declaration becomes a reference to per-workgroup
+// storage (tests/cpu_emu/build.py rewrites it); `key` is unique per
+// declaration and template instantiation.
+template <typename T>
+inline T& lds(const void* key) {
+  return *static_cast<T*>(lds_slot(key, sizeof(T)));
+}
 int cu_count();
 void set_last_error(hipError_t e);
 hipError_t take_last_error();

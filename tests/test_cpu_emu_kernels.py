@@ -11,11 +11,12 @@ against the oracle to the GPU tests' bar:
     GPU tests' bounds (the emulation's exp2 / rcp are libm's, about an ulp
     from the hardware's).
 
-What this does not show: timing, and behaviour that depends on several
-workgroups running at once (one workgroup runs at a time). LDS DMA completes
-at issue here; child processes rerun a case of every family with each DMA
-landing only at its wave's wait and the work-items in random order, and on
-an AddressSanitizer build. Every DMA
+What this does not show: timing, the GPU memory model across XCDs (the
+emulation's memory is coherent), and the hardware's exp2 / rcp rounding.
+Here one workgroup runs at a time and each LDS DMA lands when issued; child
+processes rerun a case of every family with 32 workgroups interleaved in
+random order, DMA landing at the latest permitted time, and on an
+AddressSanitizer build. Every DMA
 tile configuration is reached at small shapes through a hook compiled into
 the emulation build only (TVQ_TEST_HOOKS), and small CU counts (EMU_CUS) make
 the persistent grid walk several tiles per workgroup.
@@ -454,13 +455,14 @@ def test_qk_norm_rope_and_kv_store(elib, dtype, t, hq, hkv):
     d, max_pos, n_slots, max_len = 128, 256, 3, 64
     g = torch.Generator().manual_seed(t + hq)
     qkv = (torch.randn(t, (hq + 2 * hkv) * d, generator=g) * 2).to(dtype)
-    pos = torch.randint(0, max_len, (t,), generator=g)
+    pairs = torch.randperm(n_slots * max_len, generator=g)[:t]   # distinct (slot, position), as the engine's
+    pos = pairs % max_len
     inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float) / d))
     fr = torch.outer(torch.arange(max_pos, dtype=torch.float), inv)
     cos, sin = fr.cos().contiguous(), fr.sin().contiguous()
     qw = (torch.rand(d, generator=g) + 0.5).to(dtype)
     kw = (torch.rand(d, generator=g) + 0.5).to(dtype)
-    slots = torch.randint(0, n_slots, (t,), generator=g)
+    slots = pairs // max_len
     kc = torch.zeros(n_slots, hkv, max_len, d, dtype=dtype)
     vc = torch.zeros_like(kc)
     q = torch.empty(t, hq, d, dtype=dtype)
@@ -477,10 +479,8 @@ def test_qk_norm_rope_and_kv_store(elib, dtype, t, hq, hkv):
         head_ulp = rf.abs().amax(-1, keepdim=True) * 2.0 ** (-7 if dtype == torch.bfloat16 else -10)
         assert torch.all((gf - rf).abs() <= 2.0001 * ulp + head_ulp + 1e-6)
     v = qkv[:, (hq + hkv) * d:].reshape(t, hkv, d)
-    last = {}
     for i in range(t):
-        last[(int(slots[i]), int(pos[i]))] = i
-    for (sl, p), i in last.items():
+        sl, p = int(slots[i]), int(pos[i])
         assert torch.equal(kc[sl, :, p], k[i]) and torch.equal(vc[sl, :, p], v[i])
 
 
@@ -663,14 +663,18 @@ def test_decode_attention_quant(elib, hq, hkv, dtype):
 def test_kernels_in_child_modes():
     """Three child processes, run concurrently, each a case of every family:
 
-      * the AddressSanitizer build (global buffers sized exactly, dynamic LDS
-        a fresh allocation per workgroup): any out-of-bounds access aborts;
-      * twice (two seeds) with every LDS DMA landing only at its wave's vmcnt
-        wait, the latest the hardware may complete it, and the work-items in
-        a seeded random order: a stage wait that waits too little, or a
-        cross-wave dependency without a barrier, breaks parity (a stage wait
-        weakened by one stage gives wrong accumulators in this mode and none
-        in the default one)."""
+      * the AddressSanitizer build (global buffers sized exactly, LDS a fresh
+        allocation per workgroup): any out-of-bounds access aborts;
+      * 32 workgroups resident at once, in a seeded random order, stalled at
+        random so that they drift apart, with every LDS DMA landing only at
+        its wave's vmcnt wait (the latest the hardware may complete it): a
+        stage wait that waits too little, a cross-wave dependency without a
+        barrier, or a cross-workgroup handoff that assumes an arrival order
+        breaks parity (a stage wait weakened by one stage gives wrong
+        accumulators in this mode and none in the default one; picking the
+        attention rows' quantizer by head index instead of by the arrival
+        counter gives wrong codes with 32 resident workgroups);
+      * the same interleaving with a second seed and DMA landing at issue."""
     sys.path.insert(0, str(ROOT / "tests" / "cpu_emu"))
     import build as emu_build
     emu.ensure_built(asan=True)
@@ -681,8 +685,8 @@ def test_kernels_in_child_modes():
         "asan": ([script, "--asan"], dict(base, LD_PRELOAD=emu_build.asan_runtime(),
                                           ASAN_OPTIONS="detect_leaks=0:detect_stack_use_after_return=0:"
                                                        "abort_on_error=1")),
-        "late-dma-seed1": ([script], dict(base, EMU_DMA="late", EMU_SHUFFLE="1")),
-        "late-dma-seed2": ([script], dict(base, EMU_DMA="late", EMU_SHUFFLE="2")),
+        "concurrent-late-dma": ([script], dict(base, EMU_DMA="late", EMU_SHUFFLE="1", EMU_CONCURRENT="32")),
+        "concurrent": ([script], dict(base, EMU_SHUFFLE="2", EMU_CONCURRENT="32")),
     }
     procs = {k: subprocess.Popen([sys.executable, *a], env=e, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
                                  text=True) for k, (a, e) in runs.items()}
