@@ -7,6 +7,10 @@
 // fixups, the attention kernels' fused quantization) meet in whatever order
 // the interleaving produces. Each resident workgroup has its own LDS: the
 // dynamic allocation and every static __shared__ array (see lds_slot).
+// With one resident workgroup (the default), the workgroups of a launch are
+// independent of each other's timing and are spread over EMU_THREADS OS
+// threads (default: the host's CPUs, at most 8), each with its own scheduler.
+#include <setjmp.h>
 #include <stdio.h>
 #include <sys/mman.h>
 #include <ucontext.h>
@@ -14,6 +18,7 @@
 #include <algorithm>
 #include <deque>
 #include <random>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -39,9 +44,15 @@ constexpr size_t kStack = 256 << 10;
 
 struct Block;
 
+// Switches: a fiber starts on its own stack through ucontext (once); after
+// that, scheduler and fiber switch with _setjmp / _longjmp, which unlike
+// swapcontext make no signal-mask system call. The AddressSanitizer build
+// keeps swapcontext throughout (its fiber annotations assume it).
 struct Fiber {
   Lane lane;
   ucontext_t ctx;
+  jmp_buf jb;
+  bool started = false;
   char* stack = nullptr;
   Block* blk = nullptr;
 };
@@ -62,14 +73,14 @@ struct Block {
   bool active = false;
 };
 
-ucontext_t g_sched;
-const void* g_sched_stack_bottom = nullptr;
-size_t g_sched_stack_size = 0;
-Block* g_blk = nullptr;
-Fiber* g_cur = nullptr;
-const std::function<void()>* g_body = nullptr;
+thread_local ucontext_t g_sched;
+thread_local jmp_buf g_sched_jb;
+thread_local const void* g_sched_stack_bottom = nullptr;
+thread_local size_t g_sched_stack_size = 0;
+thread_local Block* g_blk = nullptr;
+thread_local Fiber* g_cur = nullptr;
+const std::function<void()>* g_body = nullptr;  // the running launch's kernel call (read-only while it runs)
 hipError_t g_err = hipSuccess;
-std::vector<Fiber> g_pool;
 
 void dma_flush_wave(Block& b, int w, int keep_ops) {
   std::deque<DmaOp>& q = b.dma[w];
@@ -88,10 +99,27 @@ void dma_flush_wave(Block& b, int w, int keep_ops) {
 void to_sched() {
 #ifdef EMU_ASAN
   __sanitizer_start_switch_fiber(nullptr, g_sched_stack_bottom, g_sched_stack_size);
-#endif
   swapcontext(&g_cur->ctx, &g_sched);
-#ifdef EMU_ASAN
   __sanitizer_finish_switch_fiber(nullptr, nullptr, nullptr);
+#else
+  if (!_setjmp(g_cur->jb)) _longjmp(g_sched_jb, 1);
+#endif
+}
+
+// Scheduler side: run fiber f until it blocks or ends.
+void switch_to(Fiber* f) {
+#ifdef EMU_ASAN
+  __sanitizer_start_switch_fiber(nullptr, f->stack, kStack);
+  swapcontext(&g_sched, &f->ctx);
+  __sanitizer_finish_switch_fiber(nullptr, nullptr, nullptr);
+#else
+  if (!_setjmp(g_sched_jb)) {
+    if (!f->started) {
+      f->started = true;
+      setcontext(&f->ctx);
+    }
+    _longjmp(f->jb, 1);
+  }
 #endif
 }
 
@@ -103,8 +131,10 @@ void fiber_entry() {
   g_cur->lane.state = kDone;
 #ifdef EMU_ASAN
   __sanitizer_start_switch_fiber(nullptr, g_sched_stack_bottom, g_sched_stack_size);
-#endif
   setcontext(&g_sched);
+#else
+  _longjmp(g_sched_jb, 1);
+#endif
 }
 
 void start_block(Block& b, Fiber* fibers, dim3 bid, size_t shmem) {
@@ -125,6 +155,7 @@ void start_block(Block& b, Fiber* fibers, dim3 bid, size_t shmem) {
     f.lane.lane = i % 64;
     f.lane.state = kRun;
     f.lane.fn = nullptr;
+    f.started = false;
     getcontext(&f.ctx);
     f.ctx.uc_stack.ss_sp = f.stack;
     f.ctx.uc_stack.ss_size = kStack;
@@ -228,38 +259,35 @@ hipError_t take_last_error() {
   return e;
 }
 
-void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body) {
+namespace {
+
+// Run workgroups first, first + stride, ... of the launch, `conc` resident
+// at a time, on this thread.
+void run_range(dim3 grid, dim3 block, size_t shmem, long first, long stride, int conc_req) {
   const long n = (long)block.x * block.y * block.z;
-  if (n <= 0 || n > 1024 || grid.x == 0 || grid.y == 0 || grid.z == 0 || shmem > (160u << 10)) {
-    set_last_error(hipErrorInvalidConfiguration);
-    return;
-  }
   const long nblocks = (long)grid.x * grid.y * grid.z;
-  static const char* conc_env = getenv("EMU_CONCURRENT");
-  const int conc = (int)std::max(1L, std::min(nblocks, conc_env ? (long)atoi(conc_env) : 1L));
-  if ((long)g_pool.size() < n * conc) {
-    const size_t old = g_pool.size();
-    g_pool.resize(n * conc);
-    for (size_t i = old; i < g_pool.size(); ++i) {
-      void* s = mmap(nullptr, kStack, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
-      if (s == MAP_FAILED) abort();
-      g_pool[i].stack = static_cast<char*>(s);
-    }
+  const long mine = first < nblocks ? (nblocks - first + stride - 1) / stride : 0;
+  if (mine == 0) return;
+  const int conc = (int)std::max(1L, std::min(mine, (long)conc_req));
+  std::vector<Fiber> pool(n * conc);
+  for (Fiber& f : pool) {
+    void* st = mmap(nullptr, kStack, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+    if (st == MAP_FAILED) abort();
+    f.stack = static_cast<char*>(st);
   }
   static const char* shuffle = getenv("EMU_SHUFFLE");
   static std::mt19937 rng(shuffle ? (unsigned)atoi(shuffle) : 0u);
-  const std::function<void()>* saved_body = g_body;
-  g_body = &body;
   std::vector<Block> slots(conc);
-  long next = 0;
-  auto bid_of = [&](long i) {
+  long next = 0;  // index into this thread's workgroups
+  auto bid_of = [&](long j) {
+    const long i = first + j * stride;
     return dim3((unsigned)(i % grid.x), (unsigned)((i / grid.x) % grid.y), (unsigned)(i / ((long)grid.x * grid.y)));
   };
   for (int s = 0; s < conc; ++s) {
     slots[s].bdim = block;
     slots[s].gdim = grid;
     slots[s].n = (int)n;
-    start_block(slots[s], &g_pool[s * n], bid_of(next++), shmem);
+    start_block(slots[s], &pool[s * n], bid_of(next++), shmem);
   }
   // One step of a resident workgroup: run its runnable fibers (each until it
   // blocks); else resolve its waves' pending wave-level operations; else
@@ -275,13 +303,7 @@ void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& 
     for (Fiber* f : order) {
       g_cur = f;
       g_blk = f->blk;
-#ifdef EMU_ASAN
-      __sanitizer_start_switch_fiber(nullptr, f->stack, kStack);
-#endif
-      swapcontext(&g_sched, &f->ctx);
-#ifdef EMU_ASAN
-      __sanitizer_finish_switch_fiber(nullptr, nullptr, nullptr);
-#endif
+      switch_to(f);
       g_cur = nullptr;
     }
     if (!order.empty()) return true;
@@ -293,7 +315,7 @@ void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& 
     }
     if (live == 0) {
       finish_block(b);
-      if (next < nblocks) start_block(b, &g_pool[s * n], bid_of(next++), shmem);
+      if (next < mine) start_block(b, &pool[s * n], bid_of(next++), shmem);
       return true;
     }
     if (at_bar == live) {
@@ -325,8 +347,36 @@ void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& 
       abort();
     }
   }
-  g_body = saved_body;
+  for (Fiber& f : pool) munmap(f.stack, kStack);
   g_blk = nullptr;
+}
+
+}  // namespace
+
+void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body) {
+  const long n = (long)block.x * block.y * block.z;
+  if (n <= 0 || n > 1024 || grid.x == 0 || grid.y == 0 || grid.z == 0 || shmem > (160u << 10)) {
+    set_last_error(hipErrorInvalidConfiguration);
+    return;
+  }
+  const long nblocks = (long)grid.x * grid.y * grid.z;
+  static const char* conc_env = getenv("EMU_CONCURRENT");
+  static const char* thr_env = getenv("EMU_THREADS");
+  const int conc = conc_env ? std::max(1, atoi(conc_env)) : 1;
+  int threads = thr_env ? std::max(1, atoi(thr_env))
+                        : (int)std::min(8u, std::max(1u, std::thread::hardware_concurrency()));
+  if (conc > 1 || nblocks < 2) threads = 1;  // interleaved workgroups share one scheduler
+  threads = (int)std::min<long>(threads, nblocks);
+  const std::function<void()>* saved_body = g_body;
+  g_body = &body;
+  if (threads == 1) {
+    run_range(grid, block, shmem, 0, 1, conc);
+  } else {
+    std::vector<std::thread> ts;
+    for (int t = 0; t < threads; ++t) ts.emplace_back(run_range, grid, block, shmem, (long)t, (long)threads, 1);
+    for (auto& t : ts) t.join();
+  }
+  g_body = saved_body;
 }
 
 }  // namespace emu
