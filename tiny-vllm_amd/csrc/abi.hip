@@ -88,21 +88,59 @@ namespace {
 // the shapes it supports (others keep the automatic choice). A diagnostic for
 // benchmarks and for tests that compare the families on the same inputs.
 bool forced_path(const GemmArgs& a, Path* out) {
-  const char* env = getenv("TVQ_GEMM_PATH");
-  if (env == nullptr || env[0] == 0) return false;
-  Path p;
+  const int f = switches().gemm_path;
+  if (f < 0) return false;
+  const Path p = (Path)f;
   bool ok;
-  if (!strcmp(env, "gemv")) p = Path::kGemv, ok = gemv_shape_ok(a.M, a.K);
-  else if (!strcmp(env, "skinny")) p = Path::kSkinny, ok = a.M <= kSkinnyMaxM;
-  else if (!strcmp(env, "stream")) p = Path::kStream, ok = stream_shape_ok(a.M, a.N, a.K);
-  else if (!strcmp(env, "dma")) p = Path::kDma, ok = dma_shape_ok(a.K);
-  else return false;
+  if (p == Path::kGemv) ok = gemv_shape_ok(a.M, a.K);
+  else if (p == Path::kSkinny) ok = a.M <= kSkinnyMaxM;
+  else if (p == Path::kStream) ok = stream_shape_ok(a.M, a.N, a.K);
+  else ok = dma_shape_ok(a.K);
   if (!ok) return false;
   *out = p;
   return true;
 }
 
+thread_local const Switches* t_switches = nullptr;
+
 }  // namespace
+
+Switches read_switches() {
+  Switches w{-1, false, 8, false};
+  if (const char* e = getenv("TVQ_GEMM_PATH")) {
+    if (!strcmp(e, "gemv")) w.gemm_path = (int)Path::kGemv;
+    else if (!strcmp(e, "skinny")) w.gemm_path = (int)Path::kSkinny;
+    else if (!strcmp(e, "stream")) w.gemm_path = (int)Path::kStream;
+    else if (!strcmp(e, "dma")) w.gemm_path = (int)Path::kDma;
+  }
+  const char* sk = getenv("TVQ_STREAMK");
+  w.streamk = sk != nullptr && sk[0] == '1';
+  if (const char* e = getenv("TVQ_STREAMK_MIN")) {
+    const int v = atoi(e);
+    if (v >= 1 && v <= 64) w.streamk_min = v;
+  }
+  const char* w4 = getenv("TVQ_PREFILL_W4");
+  w.prefill_w4 = w4 != nullptr && w4[0] == '1';
+  return w;
+}
+
+const Switches& switches() {
+  if (t_switches != nullptr) return *t_switches;
+  thread_local Switches fresh;
+  fresh = read_switches();
+  return fresh;
+}
+
+SwitchScope::SwitchScope() : snap_(), owner_(t_switches == nullptr) {
+  if (owner_) {
+    snap_ = read_switches();
+    t_switches = &snap_;
+  }
+}
+
+SwitchScope::~SwitchScope() {
+  if (owner_) t_switches = nullptr;
+}
 
 Path select_gemm_path(const GemmArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.qweight) && aligned16(a.y) && shape_vec_ok(a.K);
@@ -154,6 +192,7 @@ int tvq_abi_version(void) { return TVQ_ABI_VERSION; }
 const char* tvq_last_error(void) { return g_last_error.c_str(); }
 
 const char* tvq_select_path(int op, int64_t M, int64_t N, int64_t K, int dtype) {
+  SwitchScope switch_scope;
   (void)dtype;
   switch (op) {
     case TVQ_OP_ACT_QUANT: return (K % 8 == 0) ? "act_quant_vec" : "act_quant_scalar";
@@ -179,6 +218,7 @@ int64_t tvq_gemm_workspace_bytes(void) { return kGemmWorkspaceBytes; }
 
 int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight, const float* scales, const void* bias, void* y,
                    int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+  SwitchScope switch_scope;
   if (int rc = check_dtype(dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
   if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
@@ -192,6 +232,7 @@ int tvq_w8a16_gemm(const void* x, int dtype, const int8_t* qweight, const float*
 int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales, const int8_t* qweight, const float* w_scales,
                   const void* bias, void* y, int out_dtype, int64_t M, int64_t N, int64_t K, void* workspace,
                   int64_t workspace_bytes, void* stream) {
+  SwitchScope switch_scope;
   if (int rc = check_dtype(out_dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
   if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
@@ -204,6 +245,7 @@ int tvq_w8a8_gemm(const int8_t* xq, const float* a_scales, const int8_t* qweight
 
 int tvq_w8a16_gemm_rounded(const void* x, int dtype, const int8_t* qweight, const float* scales, const void* bias,
                            void* y, int64_t M, int64_t N, int64_t K, void* stream) {
+  SwitchScope switch_scope;
   if (int rc = check_dtype(dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
   if (M == 0) return ok();
@@ -218,6 +260,7 @@ int tvq_w8a16_gemm_rounded(const void* x, int dtype, const int8_t* qweight, cons
 
 int tvq_gemm_operand_floor(int op, const void* x, const int8_t* qweight, int64_t M, int64_t N, int64_t K,
                            void* stream) {
+  SwitchScope switch_scope;
   if (op != TVQ_OP_W8A16 && op != TVQ_OP_W8A8) return fail(TVQ_E_INVALID, "op must be TVQ_OP_W8A16 or TVQ_OP_W8A8");
   if (int rc = check_dims(M, N, K)) return rc;
   if (M == 0) return ok();
@@ -232,6 +275,7 @@ int tvq_gemm_operand_floor(int op, const void* x, const int8_t* qweight, int64_t
 
 int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32, int64_t M, int64_t N, int64_t K,
                       void* workspace, int64_t workspace_bytes, void* stream) {
+  SwitchScope switch_scope;
   if (int rc = check_dims(M, N, K)) return rc;
   if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
   if (M == 0) return ok();
@@ -243,6 +287,7 @@ int tvq_w8a8_gemm_i32(const int8_t* xq, const int8_t* qweight, int32_t* y_i32, i
 int tvq_w8a8_linear(const void* x, int dtype, const int8_t* qweight, const float* w_scales, const void* bias,
                     void* y, int64_t M, int64_t N, int64_t K, int8_t* xq_buf, float* a_scales_buf, void* workspace,
                     int64_t workspace_bytes, void* stream) {
+  SwitchScope switch_scope;
   if (int rc = check_dtype(dtype)) return rc;
   if (int rc = check_dims(M, N, K)) return rc;
   if (int rc = check_workspace(workspace, workspace_bytes)) return rc;
@@ -271,6 +316,7 @@ int tvq_rmsnorm(const void* x, void* residual, const void* weight, float eps, vo
 
 int tvq_w8a8_gemm_glu(const int8_t* xq, const float* a_scales, const int8_t* qweight_glu, const float* w_scales_glu,
                       void* y, int out_dtype, int64_t M, int64_t N2, int64_t K, void* stream) {
+  SwitchScope switch_scope;
   if (int rc = check_dtype(out_dtype)) return rc;
   if (int rc = check_dims(M, N2, K)) return rc;
   if (M == 0) return ok();

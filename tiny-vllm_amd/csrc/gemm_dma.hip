@@ -106,22 +106,16 @@ int64_t tiles(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm)
 // workspace): M <= 64, fewer than 16384 output channels, K >= 2048.
 bool split_shape(int64_t M, int64_t N, int64_t K) { return M <= 64 && N < 16384 && K >= 2048; }
 
-// Stream-K for decode-size M (TVQ_STREAMK=1; read per call): every CU takes
-// an equal share of the tiles' k-stages (gemm_dma_kernel.h), so shapes whose
-// tile count is not a multiple of the CU count (e.g. 192 tiles of 64x128 on
-// 256 CUs at the 8B gate_up) keep every CU's weight stream busy. It needs a
-// workspace of two accumulator images per workgroup.
-bool streamk_shape(int64_t M) {
-  const char* env = getenv("TVQ_STREAMK");
-  return M <= 64 && env != nullptr && env[0] == '1';
-}
+// Stream-K for decode-size M (TVQ_STREAMK=1): every CU takes an equal share
+// of the tiles' k-stages (gemm_dma_kernel.h), so shapes whose tile count is
+// not a multiple of the CU count (e.g. 192 tiles of 64x128 on 256 CUs at the
+// 8B gate_up) keep every CU's weight stream busy. It needs a workspace of
+// two accumulator images per workgroup.
+bool streamk_shape(int64_t M) { return M <= 64 && switches().streamk; }
 
-// TVQ_PREFILL_W4=1 (read per call): the 4-wave prefill tiles in place of the
-// 8-wave 256x256 (W8A8) and 128x256 (W8A16) ones.
-bool prefill_w4() {
-  const char* env = getenv("TVQ_PREFILL_W4");
-  return env != nullptr && env[0] == '1';
-}
+// TVQ_PREFILL_W4=1: the 4-wave prefill tiles in place of the 8-wave 256x256
+// (W8A8) and 128x256 (W8A16) ones.
+bool prefill_w4() { return switches().prefill_w4; }
 
 #ifdef TVQ_TEST_HOOKS
 // CPU-emulation builds of the tests only (never defined for the GPU library):

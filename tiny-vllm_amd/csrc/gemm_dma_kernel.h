@@ -87,6 +87,7 @@
 #include <type_traits>
 
 #include "tvq_common.h"
+#include "tvq_internal.h"
 
 // Timeline hooks for instrumented builds (no code in the library).
 #ifndef TVQ_TL_MARK
@@ -870,11 +871,7 @@ inline int choose_splits(int tiles, int nk, int cus, int tile_bytes, const void*
 // default 8); 0 when the workspace cannot hold two accumulator images per
 // workgroup or the counters (then the launch does not use stream-K). *grid
 // receives the workgroup count.
-inline int streamk_min_stages() {
-  const char* env = getenv("TVQ_STREAMK_MIN");
-  const int v = env != nullptr ? atoi(env) : 0;
-  return v >= 1 && v <= 64 ? v : 8;
-}
+inline int streamk_min_stages() { return switches().streamk_min; }
 
 inline int choose_streamk(int tiles, int nk, int cus, int tile_bytes, const void* wsp, int64_t ws_bytes, int* grid) {
   const int kMinStages = streamk_min_stages();

@@ -33,6 +33,34 @@ struct GemmArgs {
 
 bool act_quant_vec_ok(const void* x, const void* xq, int64_t K);
 
+// Environment switches of the GEMM dispatch (diagnostic / opt-in):
+//   TVQ_GEMM_PATH=gemv|skinny|stream|dma  force a kernel family where valid
+//   TVQ_STREAMK=1      stream-K for decode-size DMA shapes
+//   TVQ_STREAMK_MIN=n  stream-K: at least n k-stages per workgroup (default 8)
+//   TVQ_PREFILL_W4=1   the 4-wave prefill tiles
+// Read once per C-ABI call (SwitchScope at each GEMM entry point), so every
+// decision inside one call (path name, tile, split, launch) sees the same
+// values; outside a scope they are read afresh.
+struct Switches {
+  int gemm_path;  // -1 none, else a Path value
+  bool streamk;
+  int streamk_min;
+  bool prefill_w4;
+};
+Switches read_switches();
+const Switches& switches();  // the current call's snapshot
+class SwitchScope {
+ public:
+  SwitchScope();
+  ~SwitchScope();
+  SwitchScope(const SwitchScope&) = delete;
+  SwitchScope& operator=(const SwitchScope&) = delete;
+
+ private:
+  Switches snap_;
+  bool owner_;
+};
+
 // Attention output quantized for the W8A8 o_proj in the same launch: per-token
 // int8 codes [T, Hq*128] and fp32 scales [T], and the row-block counters of
 // the last-arrival handoff (zero on entry, left zero).
