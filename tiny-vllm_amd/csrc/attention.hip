@@ -82,7 +82,7 @@ __device__ __forceinline__ uint32_t codes4(uint64_t w, float s, float rs) {
 // [r0, r1) of the [*, W] output (W % 4 == 0). Called by every thread of the
 // workgroup after its output stores.
 template <typename T, int kThreads>
-__device__ void quantize_rows_last(const uint16_t* out, int64_t r0, int64_t r1, int W, int32_t* cnt, int arrivals,
+__device__ __forceinline__ void quantize_rows_last(const uint16_t* out, int64_t r0, int64_t r1, int W, int32_t* cnt, int arrivals,
                                    int8_t* xq, float* xs, float eps) {
   __shared__ int last;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's output stores have completed
