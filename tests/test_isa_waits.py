@@ -196,3 +196,13 @@ def test_operand_floor_kernels_touch_only_the_operands(floor_assembly):
         assert vmem, name
         checked += 1
     assert checked >= 13 * 2, checked   # every DmaCfg, unsplit and non-temporal-weight variants
+
+
+@pytest.mark.parametrize("cfg", [pytest.param(c, marks=pytest.mark.xfail(strict=True, reason="the W8A8 4-wave tile "
+                                                                         "spills VGPRs outside its MFMA loop"))
+                                 if c[0] in SPILLING else c for c in CONFIGS], ids=[c[0] for c in CONFIGS])
+def test_no_scratch_traffic_anywhere(assembly, cfg):
+    """No spill code at all (the W8A16 4-wave tile once spilled 2 VGPRs by
+    caching 16 scale vectors for its epilogue; it now reads them per use)."""
+    code = _kernel(assembly, cfg[1])
+    assert not [l for l in code if l.startswith("scratch_")], "scratch traffic"

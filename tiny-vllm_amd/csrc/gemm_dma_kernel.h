@@ -730,15 +730,27 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
       uint16_t* y = static_cast<uint16_t*>(yv);
       const bool vec = (n_out & 7) == 0;
       // Per-channel scales of this lane's columns, read once for all row
-      // slices (LDS reads of the scales were a large share of the epilogue);
-      // the bias, when there is one, is read per use.
-      f32x4 wsv[C::FN][kQ];
+      // slices (LDS reads of the scales were a large share of the epilogue).
+      // The W8A16 4-wave tile (4 x 2 fragments of 32 x 32) would cache 16
+      // vectors, 64 VGPRs next to its 128 accumulator AGPRs, and spilled 2
+      // VGPRs doing so: it reads each scale vector at its use instead and
+      // spills none. (The W8A8 4-wave tile spills either way, fewer with the
+      // cache.) The bias is always read per use.
+      constexpr bool kCacheWs = kW8A8 || C::FN * kQ <= 8;
+      f32x4 wsv[kCacheWs ? C::FN : 1][kCacheWs ? kQ : 1];
+      if constexpr (kCacheWs) {
 #pragma unroll
-      for (int i = 0; i < C::FN; ++i)
+        for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-        for (int q = 0; q < kQ; ++q)
-          wsv[i][q] = kDq ? f32x4{1.0f, 1.0f, 1.0f, 1.0f}
-                          : *reinterpret_cast<const f32x4*>(sc_w + MF * i + 8 * q + 4 * g);
+          for (int q = 0; q < kQ; ++q)
+            wsv[i][q] = kDq ? f32x4{1.0f, 1.0f, 1.0f, 1.0f}
+                            : *reinterpret_cast<const f32x4*>(sc_w + MF * i + 8 * q + 4 * g);
+      }
+      auto wscale = [&](int i, int q) -> f32x4 {
+        if constexpr (kCacheWs) return wsv[i][q];
+        else if constexpr (kDq) return f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+        else return *reinterpret_cast<const f32x4*>(sc_w + MF * i + 8 * q + 4 * g);
+      };
       const bool has_bias = bias != nullptr;
       TVQ_TL_MARK(4);
       auto epi_slices = [&](auto bias_c) {
@@ -753,10 +765,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
             for (int q = 0; q < kQ; ++q) {
               const int nl = 8 * q + 4 * g;  // output column within the wave tile
               float o[4];
+              const f32x4 wg = wscale(0, q), wu = wscale(1, q);
 #pragma unroll
               for (int t = 0; t < 4; ++t) {
-                const float gt = to_float<T>(from_float<T>(epi_w8a8_nb(acc[0][j][4 * q + t], as, wsv[0][q][t])));
-                const float ut = to_float<T>(from_float<T>(epi_w8a8_nb(acc[1][j][4 * q + t], as, wsv[1][q][t])));
+                const float gt = to_float<T>(from_float<T>(epi_w8a8_nb(acc[0][j][4 * q + t], as, wg[t])));
+                const float ut = to_float<T>(from_float<T>(epi_w8a8_nb(acc[1][j][4 * q + t], as, wu[t])));
                 o[t] = silu_f(gt) * ut;
               }
               u32x2 pk;
@@ -773,14 +786,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(const void* __re
               f32x4 bv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
               if constexpr (kBias) bv = *reinterpret_cast<const f32x4*>(sc_b + nl);
               float o[4];
+              const f32x4 wv = wscale(i, q);
 #pragma unroll
               for (int t = 0; t < 4; ++t) {
                 if constexpr (kW8A8)
-                  o[t] = kBias ? epi_w8a8(acc[i][j][4 * q + t], as, wsv[i][q][t], bv[t])
-                               : epi_w8a8_nb(acc[i][j][4 * q + t], as, wsv[i][q][t]);
+                  o[t] = kBias ? epi_w8a8(acc[i][j][4 * q + t], as, wv[t], bv[t])
+                               : epi_w8a8_nb(acc[i][j][4 * q + t], as, wv[t]);
                 else
-                  o[t] = kBias ? epi_w8a16(acc[i][j][4 * q + t], wsv[i][q][t], bv[t])
-                               : epi_w8a16_nb(acc[i][j][4 * q + t], wsv[i][q][t]);
+                  o[t] = kBias ? epi_w8a16(acc[i][j][4 * q + t], wv[t], bv[t])
+                               : epi_w8a16_nb(acc[i][j][4 * q + t], wv[t]);
               }
               u32x2 pk;
               pk.x = (uint32_t)from_float<T>(o[0]) | ((uint32_t)from_float<T>(o[1]) << 16);
