@@ -364,7 +364,7 @@ def _child(cmd, timeout_s):
     return None
 
 
-def run_e2e(timeout_s=420):
+def run_e2e(timeout_s=300):
     """Config 5 through the engine (nanovllm.bench_e2e) in a child process:
     256 sequences, inputs and outputs uniform 100-1024, greedy, bf16 vs W8A16
     vs W8A8 on a random-init Qwen3-0.6B. Its report comes back through a JSON
@@ -405,7 +405,7 @@ def sweep_file(tag):
     return ROOT / "gpurun_out" / (f"bench_sweep_{tag}.jsonl" if tag else "bench_sweep.jsonl")
 
 
-def run_sweep_child(quick, tag, floor, timeout_s=480):
+def run_sweep_child(quick, tag, floor, timeout_s=240):
     """Configs 1-4 in a child process (`bench.py --sweep-only`), so that a
     failure there is recorded instead of losing the headline. Returns
     (records, error): the records the child completed, and None or an error."""
@@ -476,6 +476,9 @@ def main():
     ap.add_argument("--floor", action="store_true",
                     help="also time the DMA tiles' operand stream alone (tvq_gemm_operand_floor) at the headline "
                          "and for every DMA sweep entry")
+    ap.add_argument("--e2e-timeout", type=int, default=300, help="seconds allowed to the config-5 leg")
+    ap.add_argument("--sweep-timeout", type=int, default=240,
+                    help="seconds allowed to the configs 1-4 sweep (the records it completed are kept)")
     ap.add_argument("--sweep-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--profile", action="store_true",
                     help="profiling run for rocprofv3: headline kernels only, plus one 256 MiB copy kernel "
@@ -505,8 +508,9 @@ def main():
 
     # The auxiliary legs run first, each in a child process, before this
     # process touches the GPU; a failure in either is recorded in the line.
-    e2e = None if args.no_e2e else run_e2e()
-    sweep, sweep_err = (None, None) if args.no_sweep else run_sweep_child(args.quick, args.tag, args.floor)
+    e2e = None if args.no_e2e else run_e2e(args.e2e_timeout)
+    sweep, sweep_err = (None, None) if args.no_sweep else run_sweep_child(args.quick, args.tag, args.floor,
+                                                                          args.sweep_timeout)
 
     from nanovllm.quantization import _hip
     lib = _hip.load_library()
