@@ -573,7 +573,7 @@ def _counters(n=64):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2)])
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2), (32, 8)])   # 32 heads: 4096-wide rows
 def test_prefill_attention_quant(hip, elib, hq, hkv, dtype):
     """The quantizing prefill attention writes the same output as the plain
     kernel, and int8 codes / scales bit-identical to act-quant of that
@@ -613,7 +613,7 @@ def test_prefill_attention_quant(hip, elib, hq, hkv, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4), (32, 8)])   # 32 heads: 4096-wide rows
 def test_decode_attention_quant(elib, hq, hkv, dtype):
     """The quantizing decode attention: same output and cache update as the
     plain kernel, codes and scales bit-identical to act-quant of the output,
