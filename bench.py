@@ -94,6 +94,20 @@ def roofline_for(mode, m, n, k, seconds):
 
 # ---------------------------------------------------------------- inputs
 
+_WCACHE: dict = {}
+
+
+def _quantized_weights(n, k, seed):
+    """W ~ N(0, 0.02) drawn from its own seeded generator (independent of the
+    activations, so every mode and M of a shape shares it), quantized per
+    output channel: scale = absmax / 127, round-half-even."""
+    g = torch.Generator().manual_seed(seed + 1)
+    w = torch.randn(n, k, generator=g) * 0.02
+    s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+    q = torch.round(w / s[:, None]).clamp_(-127, 127).to(torch.int8)
+    return q, s
+
+
 def make_inputs(mode, m, n, k, dev, seed=0, pool_bytes=POOL_BYTES, max_copies=256):
     """BASELINE.json's synthetic operands, generated on the host from one seeded
     CPU generator (so the GPU run and the CPU baseline see the same values):
@@ -107,12 +121,16 @@ def make_inputs(mode, m, n, k, dev, seed=0, pool_bytes=POOL_BYTES, max_copies=25
         cols = torch.randperm(k, generator=g)[: max(1, k // 100)]
         x[:, cols] *= 20.0
     x = x.to(torch.bfloat16)
-    w = torch.randn(n, k, generator=g) * 0.02
-    s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
-    q = torch.round(w / s[:, None]).clamp_(-127, 127).to(torch.int8)
-    del w
     if dev is not None and torch.device(dev).type != "cpu":
-        x, q, s = x.to(dev), q.to(dev), s.to(dev)
+        x = x.to(dev)
+        key = (n, k, seed, str(dev))
+        if _WCACHE.get("key") != key:   # one shape's weights on the device at a time
+            _WCACHE.clear()
+            q, s = _quantized_weights(n, k, seed)
+            _WCACHE.update(key=key, q=q.to(dev), s=s.to(dev))
+        q, s = _WCACHE["q"], _WCACHE["s"]
+    else:
+        q, s = _quantized_weights(n, k, seed)
     wbytes = n * k + 4 * n
     copies = max(2, min(max_copies, math.ceil(pool_bytes / wbytes)))
     qs = [q] + [q.clone() for _ in range(copies - 1)]
