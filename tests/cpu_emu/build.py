@@ -11,10 +11,15 @@ host C++ cannot express:
   * extern __shared__ T name[]  ->  T* name = (T*)::emu::dyn_smem(), and a
     static __shared__ T name[..] -> a reference to this workgroup's own
     storage (::emu::lds), so concurrently resident workgroups do not share it
-and compiled with the host clang into tests/cpu_emu/_build/libtvq_emu[_asan].so,
-which exports the same C ABI as the product library (include/tvq.h).
+and compiled with the host clang into tests/cpu_emu/_build/libtvq_emu[_asan|_race].so,
+which exports the same C ABI as the product library (include/tvq.h). The
+_asan build instruments everything for AddressSanitizer. The _race build
+compiles the kernel sources with the compiler's ThreadSanitizer
+instrumentation (every memory access becomes a call) and links the calls to
+racecheck.cpp, which checks each access against the GPU's ordering rules;
+no sanitizer runtime is involved.
 
-Usage: python tests/cpu_emu/build.py [--asan]
+Usage: python tests/cpu_emu/build.py [--asan | --race]
 """
 from __future__ import annotations
 
@@ -184,11 +189,17 @@ def rewrite(src: str) -> str:
     return src
 
 
-def build(asan: bool = False, jobs: int = 8, csrc: Path = CSRC, include: Path = INCLUDE, name: str = "") -> Path:
+def _suffix(asan: bool, race: bool) -> str:
+    return "_asan" if asan else "_race" if race else ""
+
+
+def build(asan: bool = False, jobs: int = 8, csrc: Path = CSRC, include: Path = INCLUDE, name: str = "",
+          race: bool = False) -> Path:
     """Compile `csrc` (default: the package's kernel sources) into the
     emulation library; `name` gives another library name (e.g. for sources
     of another revision)."""
-    stage = BUILD / ((name or "src") + ("_asan" if asan else ""))
+    assert not (asan and race)
+    stage = BUILD / ((name or "src") + _suffix(asan, race))
     if stage.exists():
         shutil.rmtree(stage)
     (stage / "tiny-vllm_amd" / "csrc").mkdir(parents=True)
@@ -197,26 +208,30 @@ def build(asan: bool = False, jobs: int = 8, csrc: Path = CSRC, include: Path = 
         if f.suffix in (".hip", ".h"):
             (stage / "tiny-vllm_amd" / "csrc" / (f.stem + (".cpp" if f.suffix == ".hip" else ".h"))).write_text(
                 rewrite(f.read_text()))
-    flags = ["-std=c++17", "-fPIC", "-g", "-O1" if asan else "-O2", "-ffp-contract=off", "-fno-fast-math",
+    flags = ["-std=c++17", "-fPIC", "-g", "-O1" if asan or race else "-O2", "-ffp-contract=off", "-fno-fast-math",
              "-Wno-unused-value", "-Wno-ignored-attributes", "-Wno-unknown-attributes", "-Wno-unused-command-line-argument",
              "-DTVQ_TEST_HOOKS", f"-I{HERE}"]
     if asan:
         flags += ["-fsanitize=address", "-fno-omit-frame-pointer"]
+    if race:
+        flags += ["-DEMU_RACE"]
     objs = []
-    srcs = sorted((stage / "tiny-vllm_amd" / "csrc").glob("*.cpp")) + [HERE / "emu_runtime.cpp"]
+    runtime = [HERE / "emu_runtime.cpp"] + ([HERE / "racecheck.cpp"] if race else [])
+    srcs = sorted((stage / "tiny-vllm_amd" / "csrc").glob("*.cpp")) + runtime
 
     def cc(s: Path) -> Path:
         o = stage / (s.stem + ".o")
-        proc = subprocess.run([CLANG, *flags, "-c", str(s), "-o", str(o)], capture_output=True, text=True)
+        extra = ["-fsanitize=thread"] if race and s not in runtime else []
+        proc = subprocess.run([CLANG, *flags, *extra, "-c", str(s), "-o", str(o)], capture_output=True, text=True)
         if proc.returncode != 0:
             raise RuntimeError(f"emu build failed for {s.name}:\n{proc.stderr[-6000:]}")
         return o
 
     with ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(cc, srcs))
-    lib = BUILD / (f"libtvq_emu{'_' + name if name else ''}{'_asan' if asan else ''}.so")
-    link = [CLANG, "-shared", *(["-fsanitize=address", "-shared-libasan"] if asan else []), "-o", str(lib),
-            *map(str, objs)]
+    lib = BUILD / (f"libtvq_emu{'_' + name if name else ''}{_suffix(asan, race)}.so")
+    san = ["-fsanitize=address", "-shared-libasan"] if asan else []
+    link = [CLANG, "-shared", *san, "-o", str(lib), *map(str, objs)]
     proc = subprocess.run(link, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"emu link failed:\n{proc.stderr[-4000:]}")
@@ -228,12 +243,14 @@ def asan_runtime() -> str:
                           text=True, check=True).stdout.strip()
 
 
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--asan", action="store_true")
+    ap.add_argument("--race", action="store_true")
     ap.add_argument("--csrc", type=Path, default=CSRC, help="kernel source folder (default: the package's)")
     ap.add_argument("--include", type=Path, default=INCLUDE)
     ap.add_argument("--name", default="", help="library name suffix")
     a = ap.parse_args()
-    print(build(a.asan, csrc=a.csrc, include=a.include, name=a.name))
+    print(build(a.asan, csrc=a.csrc, include=a.include, name=a.name, race=a.race))
     sys.exit(0)

@@ -5,6 +5,11 @@ infrastructure), because the emulation's modes are fixed per process:
   --asan   the AddressSanitizer build, with the ASan runtime preloaded. Every
            buffer is a CPU tensor of exactly its size, so a read or write past
            any input, output, workspace or dynamic LDS allocation aborts.
+  --race   the race-checking build (tests/cpu_emu/racecheck.h), with
+           EMU_DMA=late: an access that the GPU does not order against a
+           conflicting one (a missing barrier between waves, a read of LDS
+           before its DMA landed, two workgroups of a launch touching the same
+           memory non-atomically) is reported on stderr and fails the run.
   (plain)  run with EMU_CONCURRENT=32 (workgroups interleaved),
            EMU_SHUFFLE=seed (random order, random stalls) and optionally
            EMU_DMA=late (each LDS DMA lands only at its wave's vmcnt wait): a
@@ -62,8 +67,15 @@ def _w8a8_ok(y, xq, a_s, q, s, bias=None) -> None:
     assert np.array_equal(bits16(y), yb)
 
 
+def _arg(flag: str) -> str | None:
+    return sys.argv[sys.argv.index(flag) + 1] if flag in sys.argv else None
+
+
 def main() -> None:
-    lib = emu.load(asan="--asan" in sys.argv)
+    lib_file = _arg("--lib")
+    lib = emu.load_file(lib_file) if lib_file else emu.load(asan="--asan" in sys.argv, race="--race" in sys.argv)
+    only = _arg("--only")
+    only = only.split(",") if only else None
     from nanovllm.quantization import _hip
     n_ws = lib.tvq_gemm_workspace_bytes()
     raw = torch.zeros(n_ws + 256, dtype=torch.uint8)
@@ -76,12 +88,17 @@ def main() -> None:
     torch.cuda.device = _NoDevice
     force = ctypes.c_int.in_dll(lib, "tvq_test_force_dma_cfg")
 
-    def case(name):
+    def case(name) -> bool:
+        """Announce a case; False when --only leaves it out."""
+        if only is not None and not any(name.startswith(o) for o in only):
+            return False
         print("CASE", name, flush=True)
+        return True
 
     # act-quant: vector (1, 2 and 4 waves per row) and scalar paths
     for m, k in [(3, 1024), (600, 64), (1030, 64), (5, 100), (2, 16384)]:
-        case(f"act_quant {m}x{k}")
+        if not case(f"act_quant {m}x{k}"):
+            continue
         x = make_activations(m, k, seed=m)
         q, s = _hip.act_quant(x)
         rq, rs = oracle.c_act_quant(bits16(x))
@@ -90,7 +107,8 @@ def main() -> None:
     # GEMMs through the default dispatch (GEMV, skinny, DMA, split-K, generic)
     for m, n, k in [(1, 64, 2048), (2, 72, 1024), (9, 96, 256), (40, 136, 512), (64, 128, 4096), (300, 130, 1024),
                     (7, 33, 40), (17, 16384, 128)]:
-        case(f"gemm {m}x{n}x{k}")
+        if not case(f"gemm {m}x{n}x{k}"):
+            continue
         x = make_activations(m, k, seed=n)
         q, s = make_weights(n, k, seed=k)
         bias = torch.randn(n).to(torch.bfloat16)
@@ -107,10 +125,11 @@ def main() -> None:
         bm = int(name.split("_")[1].split("x")[0])
         bn = int(name.split("x")[1].rstrip("w48"))
         for cus in ("256", "3"):
+            m, n, k = bm + bm // 2 + 3, 2 * bn + 40, 384
+            if not case(f"dma {name} cus={cus} {m}x{n}x{k}"):
+                continue
             os.environ["EMU_CUS"] = cus
             force.value = c
-            m, n, k = bm + bm // 2 + 3, 2 * bn + 40, 384
-            case(f"dma {name} cus={cus} {m}x{n}x{k}")
             x = make_activations(m, k, seed=c)
             q, s = make_weights(n, k, seed=c + 1)
             bias = torch.randn(n).to(torch.bfloat16)
@@ -130,7 +149,8 @@ def main() -> None:
     os.environ["TVQ_STREAMK_MIN"] = "2"
     os.environ["EMU_CUS"] = "5"
     for m, n, k in [(1, 512, 1024), (16, 384, 2048), (33, 1280, 512)]:
-        case(f"streamk {m}x{n}x{k}")
+        if not case(f"streamk {m}x{n}x{k}"):
+            continue
         x = make_activations(m, k, seed=m)
         q, s = make_weights(n, k, seed=n)
         _w8a16_ok(_hip.w8a16_gemm(x, q, s), x, q, s)
@@ -142,31 +162,33 @@ def main() -> None:
 
     # producers and the gate_up epilogue
     for m, k in [(7, 1024), (600, 256), (9, 1003)]:
-        case(f"producers {m}x{k}")
+        if not case(f"producers {m}x{k}"):
+            continue
         x = make_activations(m, k, seed=k)
         res = make_activations(m, k, seed=k + 1)
         _hip.rmsnorm(x, torch.ones(k, dtype=torch.bfloat16), 1e-6, residual=res, out=True, quant=True)
         _hip.silu_mul(make_activations(m, 2 * k, seed=m), out=True, quant=True)
-    case("glu")
-    from nanovllm.quantization.utils import quantize_int8_per_channel
-    qw, s = quantize_int8_per_channel(torch.randn(320, 384) * 0.02)
-    xq, a_s = _hip.act_quant(make_activations(300, 384, seed=1))
-    q2, s2 = _hip.glu_interleave(qw, s.float())
-    yref, _ = _hip.silu_mul(_hip.w8a8_gemm(xq, a_s, qw, s.float(), out_dtype=torch.bfloat16, split_k=False))
-    assert torch.equal(_hip.w8a8_gemm_glu(xq, a_s, q2, s2), yref)
+    if case("glu"):
+        from nanovllm.quantization.utils import quantize_int8_per_channel
+        qw, s = quantize_int8_per_channel(torch.randn(320, 384) * 0.02)
+        xq, a_s = _hip.act_quant(make_activations(300, 384, seed=1))
+        q2, s2 = _hip.glu_interleave(qw, s.float())
+        yref, _ = _hip.silu_mul(_hip.w8a8_gemm(xq, a_s, qw, s.float(), out_dtype=torch.bfloat16, split_k=False))
+        assert torch.equal(_hip.w8a8_gemm_glu(xq, a_s, q2, s2), yref)
 
     # no-alloc entry
-    case("noalloc")
-    x = make_activations(8, 1024, seed=3)
-    q, s = make_weights(128, 1024, seed=4)
-    y = torch.empty(8, 128, dtype=torch.bfloat16)
-    assert lib.tvq_w8a8_linear_noalloc(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None, y.data_ptr(), 8, 128, 1024,
-                                       None) == 0
+    if case("noalloc"):
+        x = make_activations(8, 1024, seed=3)
+        q, s = make_weights(128, 1024, seed=4)
+        y = torch.empty(8, 128, dtype=torch.bfloat16)
+        assert lib.tvq_w8a8_linear_noalloc(x.data_ptr(), 1, q.data_ptr(), s.data_ptr(), None, y.data_ptr(), 8, 128,
+                                           1024, None) == 0
 
     # attention and q/k-norm + rotary (exactly sized caches and tensors)
     d = 128
     for hq, hkv in [(4, 2), (8, 2), (2, 2), (6, 2)]:
-        case(f"prefill_attention {hq}/{hkv}")
+        if not case(f"prefill_attention {hq}/{hkv}"):
+            continue
         lens = [1, 65, 129]
         t = sum(lens)
         q = torch.randn(t, hq, d).to(torch.bfloat16)
@@ -193,7 +215,8 @@ def main() -> None:
         rq, rs = oracle.c_act_quant(bits16(out.view(t, -1)))
         assert np.array_equal(xq.numpy(), rq) and np.array_equal(xs.numpy(), rs) and int(cnt.abs().sum()) == 0
     for hq, hkv in [(16, 8), (16, 4)]:
-        case(f"decode_attention {hq}/{hkv}")
+        if not case(f"decode_attention {hq}/{hkv}"):
+            continue
         n_slots, max_len, b = 3, 40, 3
         kc = torch.randn(n_slots, hkv, max_len, d).to(torch.bfloat16)
         vc = torch.randn_like(kc)
@@ -219,21 +242,25 @@ def main() -> None:
                                               cnt.data_ptr(), cnt.numel(), None) == 0
         rq, rs = oracle.c_act_quant(bits16(out2.view(b, -1)))
         assert np.array_equal(xq.numpy(), rq) and np.array_equal(xs.numpy(), rs) and int(cnt.abs().sum()) == 0
-    case("qk_norm_rope")
-    t, hq, hkv, max_pos = 5, 4, 2, 64
-    qkv = torch.randn(t, (hq + 2 * hkv) * d).to(torch.bfloat16)
-    pos = torch.tensor([0, 3, 63, 7, 9], dtype=torch.int64)
-    cos = torch.rand(max_pos, d // 2)
-    sin = torch.rand(max_pos, d // 2)
-    kc = torch.zeros(2, hkv, max_pos, d, dtype=torch.bfloat16)
-    vc = torch.zeros_like(kc)
-    slots = torch.tensor([0, 1, 1, 0, 1], dtype=torch.int64)
-    qo = torch.empty(t, hq, d, dtype=torch.bfloat16)
-    ko = torch.empty(t, hkv, d, dtype=torch.bfloat16)
-    w = torch.ones(d, dtype=torch.bfloat16)
-    assert lib.tvq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-                                w.data_ptr(), w.data_ptr(), 1e-6, t, hq, hkv, d, max_pos, qo.data_ptr(), ko.data_ptr(),
-                                kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), 2, max_pos, 1, None) == 0
+    if case("qk_norm_rope"):
+        t, hq, hkv, max_pos = 5, 4, 2, 64
+        qkv = torch.randn(t, (hq + 2 * hkv) * d).to(torch.bfloat16)
+        pos = torch.tensor([0, 3, 63, 7, 9], dtype=torch.int64)
+        cos = torch.rand(max_pos, d // 2)
+        sin = torch.rand(max_pos, d // 2)
+        kc = torch.zeros(2, hkv, max_pos, d, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        slots = torch.tensor([0, 1, 1, 0, 1], dtype=torch.int64)
+        qo = torch.empty(t, hq, d, dtype=torch.bfloat16)
+        ko = torch.empty(t, hkv, d, dtype=torch.bfloat16)
+        w = torch.ones(d, dtype=torch.bfloat16)
+        assert lib.tvq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                    w.data_ptr(), w.data_ptr(), 1e-6, t, hq, hkv, d, max_pos, qo.data_ptr(),
+                                    ko.data_ptr(), kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), 2, max_pos, 1,
+                                    None) == 0
+    if "--race" in sys.argv:
+        n = lib.tvq_emu_race_reports()
+        assert n == 0, f"{n} race report(s)"
     print("all cases passed", flush=True)
 
 

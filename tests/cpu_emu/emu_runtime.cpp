@@ -23,6 +23,9 @@
 #include <vector>
 
 #include "hip/hip_runtime.h"
+#ifdef EMU_RACE
+#include "racecheck.h"
+#endif
 
 #if defined(__has_feature)
 #if __has_feature(address_sanitizer)
@@ -61,6 +64,8 @@ struct DmaOp {
   char* dst;
   const char* src;
   int size;  // -1: the start of one wave instruction (one vm op)
+  Lane* issuer;
+  uint32_t iv, seq;  // race checking: barrier interval and access position at issue
 };
 
 struct Block {
@@ -71,6 +76,8 @@ struct Block {
   std::unordered_map<const void*, void*> lds;  // static __shared__ arrays of this workgroup
   std::vector<std::deque<DmaOp>> dma;          // per wave
   bool active = false;
+  uint32_t serial = 0;    // position in the launch (race checking)
+  uint32_t interval = 0;  // workgroup barriers passed
 };
 
 thread_local ucontext_t g_sched;
@@ -79,10 +86,13 @@ thread_local const void* g_sched_stack_bottom = nullptr;
 thread_local size_t g_sched_stack_size = 0;
 thread_local Block* g_blk = nullptr;
 thread_local Fiber* g_cur = nullptr;
+thread_local uint32_t g_serial = 0;  // workgroups started in this launch
 const std::function<void()>* g_body = nullptr;  // the running launch's kernel call (read-only while it runs)
 hipError_t g_err = hipSuccess;
 
-void dma_flush_wave(Block& b, int w, int keep_ops) {
+// Land the queued DMA of wave w until at most keep_ops instructions remain
+// (`check`: the race-checking build checks each copy where it lands).
+void dma_flush_wave(Block& b, int w, int keep_ops, bool check) {
   std::deque<DmaOp>& q = b.dma[w];
   int ops = 0;
   for (const DmaOp& d : q) ops += d.size < 0;
@@ -90,7 +100,17 @@ void dma_flush_wave(Block& b, int w, int keep_ops) {
     q.pop_front();  // instruction marker
     --ops;
     while (!q.empty() && q.front().size >= 0) {
-      memcpy(q.front().dst, q.front().src, q.front().size);
+      const DmaOp& d = q.front();
+#ifdef EMU_RACE
+      if (check) {
+        race::Who who{b.serial, d.iv, b.interval, (uint16_t)w};
+        race::access(d.src, d.size, false, false, who, nullptr, d.seq);
+        race::access(d.dst, d.size, true, false, who, nullptr, d.seq);
+      }
+#else
+      (void)check;
+#endif
+      memcpy(d.dst, d.src, d.size);
       q.pop_front();
     }
   }
@@ -145,6 +165,11 @@ void start_block(Block& b, Fiber* fibers, dim3 bid, size_t shmem) {
   // filled with a NaN pattern (uninitialised LDS)
   b.smem = shmem ? malloc(shmem) : nullptr;
   if (shmem) memset(b.smem, 0xff, shmem);
+#ifdef EMU_RACE
+  b.serial = g_serial++;
+  b.interval = 0;
+  if (shmem) race::reset(b.smem, shmem);
+#endif
   b.dma.assign((b.n + 63) / 64, {});
   for (int i = 0; i < b.n; ++i) {
     Fiber& f = fibers[i];
@@ -165,7 +190,9 @@ void start_block(Block& b, Fiber* fibers, dim3 bid, size_t shmem) {
 }
 
 void finish_block(Block& b) {
-  for (size_t w = 0; w < b.dma.size(); ++w) dma_flush_wave(b, (int)w, 0);
+  // copies never waited for land at the end (their wave may have read the
+  // destination before)
+  for (size_t w = 0; w < b.dma.size(); ++w) dma_flush_wave(b, (int)w, 0, true);
   free(b.smem);
   b.smem = nullptr;
   for (auto& kv : b.lds) free(kv.second);
@@ -219,9 +246,37 @@ void* lds_slot(const void* key, size_t bytes) {
   if (p == nullptr) {
     p = aligned_alloc(1024, (bytes + 1023) / 1024 * 1024);
     memset(p, 0xff, bytes);
+#ifdef EMU_RACE
+    race::reset(p, bytes);
+#endif
   }
   return p;
 }
+
+void lane_access(Lane* l, const void* p, size_t n, bool write) {
+#ifdef EMU_RACE
+  race::Who w;
+  race::who_of(l, &w);
+  race::access(p, n, write, false, w, nullptr);
+#else
+  (void)l, (void)p, (void)n, (void)write;
+#endif
+}
+
+#ifdef EMU_RACE
+namespace race {
+bool current(Who* w, const void* addr) {
+  if (g_cur == nullptr) return false;  // host code, or the scheduler
+  if ((const char*)addr >= g_cur->stack && (const char*)addr < g_cur->stack + kStack) return false;
+  who_of(&g_cur->lane, w);
+  return true;
+}
+void who_of(Lane* l, Who* w) {
+  const Block* b = reinterpret_cast<Fiber*>(l)->blk;  // the lane is the fiber's first member
+  *w = Who{b->serial, b->interval, b->interval, (uint16_t)l->wave};
+}
+}  // namespace race
+#endif
 
 int cu_count() {
   const char* e = getenv("EMU_CUS");
@@ -244,12 +299,16 @@ bool dma_late() {
   return e != nullptr && strcmp(e, "late") == 0;
 }
 
-void dma_enqueue(int wave, char* dst, const char* src, int size) {
-  g_blk->dma[wave].push_back(DmaOp{dst, src, size});
+void dma_enqueue(Lane* issuer, char* dst, const char* src, int size) {
+  uint32_t seq = 0;
+#ifdef EMU_RACE
+  seq = race::seq();
+#endif
+  g_blk->dma[issuer->wave].push_back(DmaOp{dst, src, size, issuer, g_blk->interval, seq});
 }
 
 void wait_vm(int n) {
-  if (g_cur != nullptr && !g_blk->dma.empty()) dma_flush_wave(*g_blk, g_cur->lane.wave, n);
+  if (g_cur != nullptr && !g_blk->dma.empty()) dma_flush_wave(*g_blk, g_cur->lane.wave, n, true);
 }
 
 void set_last_error(hipError_t e) { g_err = e; }
@@ -319,6 +378,7 @@ void run_range(dim3 grid, dim3 block, size_t shmem, long first, long stride, int
       return true;
     }
     if (at_bar == live) {
+      ++b.interval;
       for (int i = 0; i < b.n; ++i)
         if (b.fibers[i].lane.state == kBar) b.fibers[i].lane.state = kRun;
       return true;
@@ -353,7 +413,7 @@ void run_range(dim3 grid, dim3 block, size_t shmem, long first, long stride, int
 
 }  // namespace
 
-void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body) {
+void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body, const void* kernel) {
   const long n = (long)block.x * block.y * block.z;
   if (n <= 0 || n > 1024 || grid.x == 0 || grid.y == 0 || grid.z == 0 || shmem > (160u << 10)) {
     set_last_error(hipErrorInvalidConfiguration);
@@ -366,6 +426,13 @@ void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& 
   int threads = thr_env ? std::max(1, atoi(thr_env))
                         : (int)std::min(8u, std::max(1u, std::thread::hardware_concurrency()));
   if (conc > 1 || nblocks < 2) threads = 1;  // interleaved workgroups share one scheduler
+#ifdef EMU_RACE
+  threads = 1;  // the checker's shadow state is not shared between threads
+  g_serial = 0;
+  race::launch_begin(kernel);
+#else
+  (void)kernel;
+#endif
   threads = (int)std::min<long>(threads, nblocks);
   const std::function<void()>* saved_body = g_body;
   g_body = &body;

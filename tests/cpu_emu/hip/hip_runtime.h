@@ -97,13 +97,13 @@ inline T& lds(const void* key) {
 int cu_count();
 void set_last_error(hipError_t e);
 hipError_t take_last_error();
-void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body);
+void run_grid(dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body, const void* kernel);
 
 template <typename... P, typename... A>
 void launch(void (*k)(P...), dim3 grid, dim3 block, size_t shmem, hipStream_t, A&&... args) {
   static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
   std::tuple<std::decay_t<P>...> t(((std::decay_t<P>)(args))...);
-  run_grid(grid, block, shmem, [&]() { std::apply(k, t); });
+  run_grid(grid, block, shmem, [&]() { std::apply(k, t); }, (const void*)k);
 }
 
 // `kern<<<...>>>` where kern is itself a function-pointer variable
@@ -112,23 +112,34 @@ void launch(void (**k)(P...), dim3 grid, dim3 block, size_t shmem, hipStream_t s
   launch(*k, grid, block, shmem, st, std::forward<A>(args)...);
 }
 
+// A wave-level operation's operands pass through the lane's in[] / out[]
+// slots, which the scheduler reads and writes between the lanes' turns: not
+// memory of the kernel, so the race-checking build leaves these copies
+// uninstrumented (the operation's own memory accesses are checked through
+// lane_access).
+#define EMU_UNCHECKED __attribute__((no_sanitize("thread")))
 template <typename T>
-inline void put(Lane* l, int slot, const T& v) {
+EMU_UNCHECKED inline void put(Lane* l, int slot, const T& v) {
   static_assert(sizeof(T) <= 64, "wave-op operand");
-  memcpy(l->in[slot], &v, sizeof(T));
+  __builtin_memcpy_inline(l->in[slot], &v, sizeof(T));
 }
 template <typename T>
-inline T get_in(const Lane* l, int slot) {
+EMU_UNCHECKED inline T get_in(const Lane* l, int slot) {
   T v;
-  memcpy(&v, l->in[slot], sizeof(T));
+  __builtin_memcpy_inline(&v, l->in[slot], sizeof(T));
   return v;
 }
 template <typename T>
-inline T get_out(const Lane* l) {
+EMU_UNCHECKED inline T get_out(const Lane* l) {
   T v;
-  memcpy(&v, l->out, sizeof(T));
+  __builtin_memcpy_inline(&v, l->out, sizeof(T));
   return v;
 }
+
+// The memory access of one lane within a wave-level operation (the scheduler
+// performs the operation for the wave): checked as that lane's access in the
+// race-checking build, a no-op otherwise.
+void lane_access(Lane* l, const void* p, size_t n, bool write);
 
 // ---- cross-lane ---------------------------------------------------------
 void wait_vm(int n);
@@ -382,6 +393,8 @@ inline void tr16_fn(Lane** L) {
     }
     memcpy(L[i]->out, r, 8);
   }
+  for (int i = 0; i < 64; ++i)
+    if (L[i]) lane_access(L[i], get_in<const short*>(L[i], 0), 8, false);  // each lane's address: 8 bytes
 }
 
 // global_load_lds: lane l copies `size` bytes from its global address to
@@ -390,7 +403,7 @@ inline void tr16_fn(Lane** L) {
 // the wave and lands only when the wave waits for it (s_waitcnt vmcnt), the
 // latest time the hardware may complete it.
 bool dma_late();
-void dma_enqueue(int wave, char* dst, const char* src, int size);
+void dma_enqueue(Lane* issuer, char* dst, const char* src, int size);
 void wait_vm(int n);  // this wave: complete queued DMA until at most n remain
 
 inline void dma_fn(Lane** L) {
@@ -401,14 +414,17 @@ inline void dma_fn(Lane** L) {
   const int size = get_in<int>(L[first], 2);
   const int off = get_in<int>(L[first], 3);
   const bool late = dma_late();
-  if (late) dma_enqueue(L[first]->wave, nullptr, nullptr, -1);  // one vm op per instruction
+  if (late) dma_enqueue(L[first], nullptr, nullptr, -1);  // one vm op per instruction
   for (int i = 0; i < 64; ++i) {
     if (!L[i]) continue;
     const char* src = get_in<const char*>(L[i], 0);
-    if (late)
-      dma_enqueue(L[first]->wave, base + off + i * size, src, size);
-    else
+    if (late) {
+      dma_enqueue(L[i], base + off + i * size, src, size);  // checked where it lands
+    } else {
+      lane_access(L[i], src, size, false);
+      lane_access(L[i], base + off + i * size, size, true);
       memcpy(base + off + i * size, src, size);
+    }
   }
 }
 }  // namespace emu

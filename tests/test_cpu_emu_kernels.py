@@ -661,7 +661,7 @@ def test_decode_attention_quant(elib, hq, hkv, dtype):
 # ---------------------------------------------------------------- child-process modes
 
 def test_kernels_in_child_modes():
-    """Three child processes, run concurrently, each a case of every family:
+    """Four child processes, run concurrently, each a case of every family:
 
       * the AddressSanitizer build (global buffers sized exactly, LDS a fresh
         allocation per workgroup): any out-of-bounds access aborts;
@@ -674,10 +674,14 @@ def test_kernels_in_child_modes():
         accumulators in this mode and none in the default one; picking the
         attention rows' quantizer by head index instead of by the arrival
         counter gives wrong codes with 32 resident workgroups);
-      * the same interleaving with a second seed and DMA landing at issue."""
+      * the same interleaving with a second seed and DMA landing at issue;
+      * the race-checking build (tests/cpu_emu/racecheck.h), DMA landing at
+        its wave's wait: no access may conflict with one the GPU does not
+        order it against (tests/test_cpu_emu_race.py shows what it catches)."""
     sys.path.insert(0, str(ROOT / "tests" / "cpu_emu"))
     import build as emu_build
     emu.ensure_built(asan=True)
+    emu.ensure_built(race=True)
     emu.ensure_built()
     base = dict(os.environ, PYTHONPATH=os.pathsep.join([str(ROOT), str(ROOT / "tiny-vllm_amd")]))
     script = str(ROOT / "tests" / "cpu_emu" / "child_cases.py")
@@ -687,6 +691,7 @@ def test_kernels_in_child_modes():
                                                        "abort_on_error=1")),
         "concurrent-late-dma": ([script], dict(base, EMU_DMA="late", EMU_SHUFFLE="1", EMU_CONCURRENT="32")),
         "concurrent": ([script], dict(base, EMU_SHUFFLE="2", EMU_CONCURRENT="32")),
+        "race": ([script, "--race"], dict(base, EMU_DMA="late")),
     }
     procs = {k: subprocess.Popen([sys.executable, *a], env=e, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
                                  text=True) for k, (a, e) in runs.items()}
@@ -694,5 +699,5 @@ def test_kernels_in_child_modes():
     for k, p in procs.items():
         out, err = p.communicate(timeout=900)
         if p.returncode != 0 or "all cases passed" not in out:
-            failed.append(f"--- {k}: rc={p.returncode}\n{out[-2000:]}\n{err[-4000:]}")
+            failed.append(f"--- {k}: rc={p.returncode}\n{out[-2000:]}\n{emu.symbolize(err[-4000:])}")
     assert not failed, "\n".join(failed)

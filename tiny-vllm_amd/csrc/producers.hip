@@ -132,13 +132,19 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t* __r
   const int vmax = nvec > 0 ? nvec - 1 : 0;
   // The norm weights are loaded with them: issued after the row reduction,
   // they added an L2 round trip to every row.
-  u32x4 xin[NI], rin[NI], win[NI];
+  // The residual is rewritten in place by the lane that owns each vector, so
+  // a lane never loads a vector of res it does not own: rows past M (the
+  // tail of the last workgroup) load nothing, and the clamped loads past the
+  // row's end read x instead (their values are never used).
+  u32x4 xin[NI] = {}, rin[NI] = {}, win[NI] = {};
+  if (rl.live) {
 #pragma unroll
-  for (int it = 0; it < NI; ++it) {
-    const int v = min(it * TPR + t, vmax);
-    xin[it] = ldg128_stream(xr + (int64_t)v * 8);
-    if constexpr (kRes) rin[it] = ldg128_stream(res + row * K + (int64_t)v * 8);
-    win[it] = ldg128(w + (int64_t)v * 8);
+    for (int it = 0; it < NI; ++it) {
+      const int v = min(it * TPR + t, vmax);
+      xin[it] = ldg128_stream(xr + (int64_t)v * 8);
+      if constexpr (kRes) rin[it] = ldg128_stream((it * TPR + t < nvec ? res + row * K : xr) + (int64_t)v * 8);
+      win[it] = ldg128(w + (int64_t)v * 8);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
 #pragma unroll
