@@ -36,7 +36,8 @@ import oracle  # noqa: E402
 from tests.helpers import bits16, make_activations, make_weights  # noqa: E402
 
 CFG = dict(kI8_256x256=0, kI8_256x128=1, kI8_64x64=2, kI8_64x128=3, kI8_32x64=4, kH_128x256=5, kH_64x128=6,
-           kH_64x64=7, kH_32x64=8, kH_64x128w8=9, kI8_256x256w4=10, kH_128x256w4=11, kH_16x128=12)
+           kH_64x64=7, kH_32x64=8, kH_64x128w8=9, kI8_256x256w4=10, kH_128x256w4=11, kH_16x128=12,
+           kH_64x256=13, kH_32x256=14)
 
 
 class _NoDevice:

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(hiplib):
 
 def test_abi_version_and_errors_without_gpu(hiplib):
     assert hiplib.tvq_abi_version() == 5
-    assert hiplib.tvq_gemm_workspace_bytes() >= 16 << 20
+    assert hiplib.tvq_gemm_workspace_bytes() >= 32 << 20  # stream-K: two 64x256 fp32 images per CU
     assert hiplib.tvq_w8a16_gemm(None, 7, None, None, None, None, 1, 1, 16, None, 0, None) == -1
     assert b"dtype" in hiplib.tvq_last_error()
     assert hiplib.tvq_w8a16_gemm(None, 1, None, None, None, None, 1, 1, 16, None, 0, None) == -1
@@ -155,9 +155,11 @@ def test_select_path_opt_in_switches(hiplib, monkeypatch):
     assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_64x64"        # decode sizes unchanged
     monkeypatch.delenv("TVQ_PREFILL_W4")
     monkeypatch.setenv("TVQ_STREAMK", "1")
-    assert sp(_hip.OP_W8A16, 64, 4096, 12288) == "dma_mfma_f16x_64x128w8"   # instead of split-K 64x64
+    assert sp(_hip.OP_W8A16, 64, 4096, 12288) == "dma_mfma_f16x_64x256"     # instead of split-K 64x64
+    assert sp(_hip.OP_W8A16, 64, 24576, 4096) == "dma_mfma_f16x_64x256"     # instead of 64x128w8
     assert sp(_hip.OP_W8A8, 48, 4096, 4096) == "dma_mfma_i8_64x128"
-    assert sp(_hip.OP_W8A16, 32, 4096, 4096) == "dma_mfma_f16x_32x64"
+    assert sp(_hip.OP_W8A16, 32, 4096, 4096) == "dma_mfma_f16x_32x256"
+    assert sp(_hip.OP_W8A16, 17, 4096, 4096) == "dma_mfma_f16x_32x256"
     assert sp(_hip.OP_W8A8, 16, 24576, 4096) == "dma_mfma_i8_32x64"
     assert sp(_hip.OP_W8A8, 256, 4096, 1024) == "dma_mfma_i8_64x64"        # M > 64 unchanged
     assert sp(_hip.OP_W8A16, 1, 4096, 1024) == "gemv_dot2_f16x"            # the GEMV keeps M <= 2

@@ -46,7 +46,8 @@ if not Path(emu.CLANG).exists():  # pragma: no cover
 
 # DmaCfg indices (gemm_dma.hip)
 CFG = dict(kI8_256x256=0, kI8_256x128=1, kI8_64x64=2, kI8_64x128=3, kI8_32x64=4, kH_128x256=5, kH_64x128=6,
-           kH_64x64=7, kH_32x64=8, kH_64x128w8=9, kI8_256x256w4=10, kH_128x256w4=11, kH_16x128=12)
+           kH_64x64=7, kH_32x64=8, kH_64x128w8=9, kI8_256x256w4=10, kH_128x256w4=11, kH_16x128=12,
+           kH_64x256=13, kH_32x256=14)
 I8_CFGS = [c for c in CFG if c.startswith("kI8")]
 H_CFGS = [c for c in CFG if c.startswith("kH")]
 

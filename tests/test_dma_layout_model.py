@@ -33,6 +33,8 @@ CONFIGS = [
     (True, 256, 256, 2, 2, 32, 64),     # 4-wave prefill tiles (TVQ_PREFILL_W4=1)
     (False, 128, 256, 2, 2, 32, 64),
     (False, 16, 128, 1, 4, 16, 128),    # W8A16 M <= 16 under stream-K (TVQ_STREAMK=1)
+    (False, 64, 256, 2, 4, 16, 128),    # W8A16 32 < M <= 64 under stream-K
+    (False, 32, 256, 2, 4, 16, 128),    # W8A16 16 < M <= 32 under stream-K
 ]
 
 

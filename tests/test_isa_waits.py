@@ -29,6 +29,8 @@ CONFIGS = [
     ("w8a8_256x256w4", "true, false, 256, 256, 2, 2, 4, 32, 64, false"),
     ("w8a16_128x256w4", "false, false, 128, 256, 2, 2, 4, 32, 64, false"),
     ("w8a16_16x128_streamk", "false, false, 16, 128, 1, 4, 4, 16, 128, true, false, false, false, false, false, true"),
+    ("w8a16_64x256_streamk", "false, false, 64, 256, 2, 4, 3, 16, 128, true, false, false, false, false, false, true"),
+    ("w8a16_32x256_streamk", "false, false, 32, 256, 2, 4, 3, 16, 128, true, false, false, false, false, false, true"),
 ]
 
 

@@ -103,14 +103,14 @@ DECODE_SHAPES = [(64, 24576, 4096), (64, 6144, 4096), (64, 4096, 4096), (64, 409
                  (64, 6144, 1024), (64, 4096, 1024), (64, 3072, 1024), (64, 1024, 3072), (64, 1024, 2048),
                  (32, 24576, 4096), (24, 4096, 4096), (17, 1000, 2048), (33, 136, 2048), (20, 4096, 12288),
                  (16, 24576, 4096), (8, 4096, 12288), (3, 6144, 4096), (13, 1000, 2048)]
-WS_BYTES = (16 << 20) + (64 << 10)   # tvq_gemm_workspace_bytes()
+WS_BYTES = (32 << 20) + (64 << 10)   # tvq_gemm_workspace_bytes()
 
 
 def streamk_tile(w8a8, m):
     """gemm_dma.hip choose() under TVQ_STREAMK=1."""
-    if m > 32:
-        return 64, 128
-    return (32, 64) if (w8a8 or m > 16) else (16, 128)
+    if w8a8:
+        return (64, 128) if m > 32 else (32, 64)
+    return (64, 256) if m > 32 else (32, 256) if m > 16 else (16, 128)
 
 
 @pytest.mark.parametrize("w8a8", [False, True])
@@ -137,10 +137,12 @@ def test_streamk_partition_sweep(tiles, nk, cus):
 
 
 def test_streamk_workspace_limit():
-    """Without room for two images per workgroup the launch does not use stream-K."""
-    tiles, nk, tb = 192, 32, 64 * 128 * 4
+    """Without room for two images per workgroup the launch does not use
+    stream-K; the default workspace is exactly full with the 64x256 W8A16
+    tiles of the 8B gate_up at M = 64 (96 tiles x 32 stages on 256 CUs)."""
+    tiles, nk, tb = 96, 32, 64 * 256 * 4
     length, grid = choose_streamk(tiles, nk, 256, tb, WS_BYTES)
-    assert length == 24 and grid == 256
+    assert length == 12 and grid == 256
     assert KSPLIT_CNT_BYTES + 2 * grid * tb <= WS_BYTES
     assert choose_streamk(tiles, nk, 256, tb, WS_BYTES - 1) == (0, 0)
     assert choose_streamk(tiles, nk, 256, tb, 0) == (0, 0)

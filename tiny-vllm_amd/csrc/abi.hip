@@ -53,8 +53,9 @@ int check_dtype(int dtype) {
 bool shape_vec_ok(int64_t K) { return K % 16 == 0; }
 
 // Recommended split-K workspace: the counter block plus the largest set of
-// partial tiles the split policy produces on a 256-CU device.
-constexpr int64_t kGemmWorkspaceBytes = (16 << 20) + (64 << 10);
+// partial tiles the split policies produce on a 256-CU device (stream-K with
+// 64x256 fp32 tiles: two 64 KiB images for each of 256 workgroups).
+constexpr int64_t kGemmWorkspaceBytes = (32 << 20) + (64 << 10);
 
 int check_workspace(const void* ws, int64_t bytes) {
   if (ws == nullptr) return TVQ_OK;

@@ -17,6 +17,8 @@
 //                                        than 4 waves of 32x32x16 at the 8B gate_up shape)
 //         M <= 64                        32x64,   4 waves,       S=4, 16x16x32 bf16
 //         otherwise                      64x64,   4 waves,       S=4, 32x32x16
+// Stream-K (TVQ_STREAMK=1, M <= 64): W8A8 64x128 (M > 32) / 32x64; W8A16
+// 64x256 (M > 32), 32x256 (M > 16), 16x128 (M <= 16).
 // For 16 < M <= 64 these tiles beat the skinny kernel, whose 16-channel
 // workgroups re-read all M activation rows per workgroup (8x the weight
 // traffic at M = 64).
@@ -40,7 +42,7 @@ using dma::launch_dma;
 
 enum class DmaCfg {
   kI8_256x256, kI8_256x128, kI8_64x64, kI8_64x128, kI8_32x64, kH_128x256, kH_64x128, kH_64x64, kH_32x64, kH_64x128w8,
-  kI8_256x256w4, kH_128x256w4, kH_16x128
+  kI8_256x256w4, kH_128x256w4, kH_16x128, kH_64x256, kH_32x256
 };
 
 // Tile BM x BN, waves WM x WN, ring depth S, MFMA tile MF, per DmaCfg.
@@ -82,9 +84,17 @@ constexpr CfgInfo kInfo[] = {
     // activation panel is a quarter of the weight bytes (2 * 16 / 128)
     {false, 16, 128, 1, 4, 4, 16, 128, "dma_mfma_f16x_16x128", "dma_mfma_f16x_16x128_splitk",
      "dma_mfma_f16x_16x128_streamk"},
+    // W8A16 at 16 < M <= 64 under stream-K: 256 output channels per tile, so
+    // the bf16 activation panel a tile re-reads is half (M = 64) or a quarter
+    // (M = 32) of its weight bytes, where the 64x128 tile reads as many
+    // activation bytes as weight bytes; 48 / 40 KB stages, 3-deep ring
+    {false, 64, 256, 2, 4, 3, 16, 128, "dma_mfma_f16x_64x256", "dma_mfma_f16x_64x256_splitk",
+     "dma_mfma_f16x_64x256_streamk"},
+    {false, 32, 256, 2, 4, 3, 16, 128, "dma_mfma_f16x_32x256", "dma_mfma_f16x_32x256_splitk",
+     "dma_mfma_f16x_32x256_streamk"},
 };
 
-static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_16x128 + 1, "one entry per DmaCfg");
+static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == (int)DmaCfg::kH_32x256 + 1, "one entry per DmaCfg");
 static_assert(kInfo[(int)DmaCfg::kI8_32x64].bm == 32 && kInfo[(int)DmaCfg::kH_128x256].bn == 256 &&
                   !kInfo[(int)DmaCfg::kH_64x64].w8a8 && kInfo[(int)DmaCfg::kI8_64x128].bn == 128,
               "kInfo follows the DmaCfg order");
@@ -135,7 +145,7 @@ DmaCfg choose(bool w8a8, int64_t M, int64_t N, int64_t K, bool opt_in = true) {
   if (opt_in && streamk_shape(M)) {
     // the widest decode tiles: activation traffic per weight byte 2M/BN (W8A16), M/BN (W8A8)
     if (w8a8) return M > 32 ? DmaCfg::kI8_64x128 : DmaCfg::kI8_32x64;
-    return M > 32 ? DmaCfg::kH_64x128w8 : (M > 16 ? DmaCfg::kH_32x64 : DmaCfg::kH_16x128);
+    return M > 32 ? DmaCfg::kH_64x256 : (M > 16 ? DmaCfg::kH_32x256 : DmaCfg::kH_16x128);
   }
   const bool split = split_shape(M, N, K);
   if (w8a8) {
@@ -198,7 +208,7 @@ int splits_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64_
   case DmaCfg::C: return splits_of<DmaCfg::C>(M, N, K, ws, ws_bytes);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
-    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128) TVQ_CASE(kH_64x256) TVQ_CASE(kH_32x256)
 #undef TVQ_CASE
   }
   return 1;
@@ -210,7 +220,7 @@ int streamk_for(DmaCfg c, int64_t M, int64_t N, int64_t K, const void* ws, int64
   case DmaCfg::C: return streamk_len<DmaCfg::C>(M, N, K, ws, ws_bytes);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
-    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128) TVQ_CASE(kH_64x256) TVQ_CASE(kH_32x256)
 #undef TVQ_CASE
   }
   return 0;
@@ -262,6 +272,8 @@ hipError_t run(const GemmArgs& a, hipStream_t s) {
       case DmaCfg::kH_128x256: return go<T, false, DmaCfg::kH_128x256>(a, s);
       case DmaCfg::kH_128x256w4: return go<T, false, DmaCfg::kH_128x256w4>(a, s);
       case DmaCfg::kH_16x128: return go<T, false, DmaCfg::kH_16x128>(a, s);
+      case DmaCfg::kH_64x256: return go<T, false, DmaCfg::kH_64x256>(a, s);
+      case DmaCfg::kH_32x256: return go<T, false, DmaCfg::kH_32x256>(a, s);
       case DmaCfg::kH_64x128: return go<T, false, DmaCfg::kH_64x128>(a, s);
       case DmaCfg::kH_32x64: return go<T, false, DmaCfg::kH_32x64>(a, s);
       case DmaCfg::kH_64x128w8: return go<T, false, DmaCfg::kH_64x128w8>(a, s);
@@ -353,7 +365,7 @@ hipError_t launch_dma_floor(const GemmArgs& a, hipStream_t stream) {
   case DmaCfg::C: return floor_of<DmaCfg::C>(a, stream);
     TVQ_CASE(kI8_256x256) TVQ_CASE(kI8_256x128) TVQ_CASE(kI8_64x64) TVQ_CASE(kI8_64x128) TVQ_CASE(kI8_32x64)
     TVQ_CASE(kH_128x256) TVQ_CASE(kH_64x128) TVQ_CASE(kH_64x64) TVQ_CASE(kH_32x64) TVQ_CASE(kH_64x128w8)
-    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128)
+    TVQ_CASE(kI8_256x256w4) TVQ_CASE(kH_128x256w4) TVQ_CASE(kH_16x128) TVQ_CASE(kH_64x256) TVQ_CASE(kH_32x256)
 #undef TVQ_CASE
   }
   return hipErrorInvalidValue;
