@@ -18,6 +18,9 @@ Cases (prints "all cases passed" at the end):
     q/k-norm + rotary kernel, decode attention appending one row per step)
     equals a cache-free recomputation wherever the top-2 logits are clear;
   * the device path's logits stay close to the host (torch) path's.
+
+With --race (and EMU_DMA=late) it runs on the race-checking build
+(tests/cpu_emu/racecheck.h) and fails on any report.
 """
 from __future__ import annotations
 
@@ -75,7 +78,7 @@ class _NoDevice:
 
 def device_path_on_emulation():
     """From here on the model takes its device path, on the emulated kernels."""
-    lib = emu.load()
+    lib = emu.load(race="--race" in sys.argv)
     n = lib.tvq_gemm_workspace_bytes()
     raw = torch.zeros(n + 256, dtype=torch.uint8)
     off = (-raw.data_ptr()) % 256
@@ -221,6 +224,9 @@ def main() -> None:
     check_projections(build("w8a8", QWEN3_06B, 0.02), "w8a8", 28, list(range(100, 100 + 7 * 60, 7)) + [9] * 37,
                       sample_layers=(0, 13, 27))
 
+    if "--race" in sys.argv:
+        n = _hip.load_library().tvq_emu_race_reports()
+        assert n == 0, f"{n} race report(s)"
     print("all cases passed", flush=True)
 
 

@@ -16,10 +16,15 @@ on the GPU, checked against the oracle to the GPU tests' bar:
 Inputs follow BASELINE: X ~ N(0,1) (W8A8: 1% outlier columns x20), W ~
 N(0, 0.02) quantized per output channel. The emulation does not time
 anything; tests/test_gpu_configs.py holds the same shapes for the GPU.
+
+TVQ_EMU_RACE=1 (with EMU_DMA=late) runs the same cases on the race-checking
+build (tests/cpu_emu/racecheck.h), single-threaded, and fails a case that
+produces a race report.
 """
 from __future__ import annotations
 
 import functools
+import os
 import sys
 from pathlib import Path
 
@@ -38,9 +43,20 @@ if not Path(emu.CLANG).exists():  # pragma: no cover
     pytest.skip("host clang of the ROCm toolchain not found", allow_module_level=True)
 
 
+RACE = os.environ.get("TVQ_EMU_RACE") == "1"
+
+
 @pytest.fixture(scope="module")
 def lib():
-    return emu.load()
+    return emu.load(race=RACE)
+
+
+@pytest.fixture(autouse=True)
+def _no_race_reports(lib):
+    before = lib.tvq_emu_race_reports() if RACE else 0
+    yield
+    if RACE:
+        assert lib.tvq_emu_race_reports() == before, "race report(s): see stderr"
 
 
 _WS = {}
