@@ -541,7 +541,7 @@ def _prefill_ref(q, k, v, lens, scale):
     return out
 
 
-@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2)])
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2), (24, 4)])   # GQA ratios 2, 4, 1, 3, 6
 def test_prefill_attention(hip, elib, hq, hkv):
     """GQA ratio 2 and 4: the 32-query DMA kernel; 1 and 3: the 16-query one."""
     dtype = torch.bfloat16
@@ -574,7 +574,7 @@ def _counters(n=64):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2), (32, 8)])   # 32 heads: 4096-wide rows
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (2, 2), (6, 2), (24, 4), (32, 8)])   # 32 heads: 4096-wide rows
 def test_prefill_attention_quant(hip, elib, hq, hkv, dtype):
     """The quantizing prefill attention writes the same output as the plain
     kernel, and int8 codes / scales bit-identical to act-quant of that
