@@ -19,10 +19,22 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X); run with -m gpu")
 
 
+# TVQ_GPU_TESTS_ON_EMU=1: the -m gpu tests run on the CPU emulation of the
+# kernels (tests/cpu_emu/gpu_on_emu.py), CPU tensors standing in for device ones.
+ON_EMU = os.environ.get("TVQ_GPU_TESTS_ON_EMU") == "1"
+if ON_EMU:
+    sys.path.insert(0, str(ROOT / "tests" / "cpu_emu"))
+    import emu
+    import gpu_on_emu
+    gpu_on_emu.install(emu.load())
+
+
 @pytest.fixture(scope="session")
 def hiplib():
     """The built C-ABI library (built on demand if absent)."""
     from nanovllm.quantization import _hip
+    if ON_EMU:
+        return _hip.load_library()
     if not _hip.library_path().is_file():
         sys.path.insert(0, str(PKG))
         import build as tvq_build

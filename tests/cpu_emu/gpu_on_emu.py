@@ -1,0 +1,121 @@
+"""Run the GPU test files (tests/test_gpu_*.py, -m gpu) on the CPU emulation
+of the kernels: test infrastructure, enabled by TVQ_GPU_TESTS_ON_EMU=1
+through tests/conftest.py, e.g.
+
+    TVQ_GPU_TESTS_ON_EMU=1 python -m pytest tests -m gpu -k parity
+
+The emulated library (tests/cpu_emu/build.py) takes host pointers, so CPU
+tensors stand in for device tensors:
+  * a TorchFunctionMode maps every device="cuda" argument (factories,
+    Tensor.to, Tensor.cuda) to the CPU, and pin_memory to a no-op;
+  * every tensor reports is_cuda, so the package takes its device path;
+  * torch.cuda's synchronisation, streams, device and memory queries become
+    host no-ops; HIP-graph capture is not emulated, so a test that captures
+    one is skipped at that point;
+  * nanovllm.quantization._hip loads the emulated library, with a 256-byte
+    aligned workspace.
+The tests' own checks then run unchanged against the kernels' emulation.
+Random data differ from a GPU run (CPU generators), and nothing is timed.
+"""
+from __future__ import annotations
+
+import contextlib
+import types
+
+import pytest
+import torch
+from torch.overrides import TorchFunctionMode
+
+
+def _is_cuda(d) -> bool:
+    if isinstance(d, torch.device):
+        return d.type == "cuda"
+    return isinstance(d, str) and d.startswith("cuda")
+
+
+class _CudaAsCpu(TorchFunctionMode):
+    def __torch_function__(self, func, types_, args=(), kwargs=None):
+        kwargs = dict(kwargs or {})
+        if func is torch.Tensor.cuda or func is torch.Tensor.pin_memory:
+            return args[0]
+        if _is_cuda(kwargs.get("device")):
+            kwargs["device"] = "cpu"
+        if kwargs.get("pin_memory"):
+            kwargs["pin_memory"] = False
+        if func is torch.Tensor.to:
+            args = tuple("cpu" if _is_cuda(a) else a for a in args)
+        return func(*args, **kwargs)
+
+
+class _Stream:
+    cuda_stream = 0
+
+    def __init__(self, *a, **k):
+        pass
+
+    def wait_stream(self, *a):
+        pass
+
+    def synchronize(self):
+        pass
+
+    def record_event(self, *a, **k):
+        return None
+
+
+def _no_graphs(*a, **k):
+    pytest.skip("HIP-graph capture is not emulated")
+
+
+_GENERATOR = torch.Generator
+_installed = False
+
+
+def install(lib) -> None:
+    """Make this process's torch treat the CPU as the GPU and point the
+    package at the emulated library `lib`."""
+    global _installed
+    if _installed:
+        return
+    _installed = True
+    _CudaAsCpu().__enter__()
+    torch.Tensor.is_cuda = property(lambda self: True)
+
+    def generator(device="cpu"):
+        return _GENERATOR(device="cpu" if _is_cuda(device) else device)
+
+    torch.Generator = generator
+    c = torch.cuda
+    c.is_available = lambda: True
+    c.device_count = lambda: 1
+    c.current_device = lambda: 0
+    c.set_device = lambda *a: None
+    c.synchronize = lambda *a, **k: None
+    c.device = lambda *a, **k: contextlib.nullcontext()
+    c.current_stream = lambda *a, **k: _Stream()
+    c.default_stream = lambda *a, **k: _Stream()
+    c.Stream = _Stream
+    c.stream = lambda *a, **k: contextlib.nullcontext()
+    c.is_current_stream_capturing = lambda: False
+    c.CUDAGraph = _no_graphs
+    c.graph = _no_graphs
+    c.empty_cache = lambda: None
+    c.mem_get_info = lambda *a: (256 << 30, 288 << 30)
+    c.memory_stats = lambda *a: {}
+    c.reset_peak_memory_stats = lambda *a: None
+    c.max_memory_allocated = lambda *a: 0
+    c.manual_seed = lambda *a: None
+    c.manual_seed_all = lambda *a: None
+    c.get_device_properties = lambda *a: types.SimpleNamespace(name="CPU emulation of gfx950",
+                                                               multi_processor_count=256,
+                                                               total_memory=288 << 30)
+
+    from nanovllm.quantization import _hip
+    n = lib.tvq_gemm_workspace_bytes()
+    raw = torch.zeros(n + 256, dtype=torch.uint8)
+    off = (-raw.data_ptr()) % 256
+    ws = raw[off:off + n]
+    _hip.load_library = lambda: lib
+    _hip._stream = lambda dev: None
+    _hip.gemm_workspace = lambda dev: ws
+    _hip._emu_keep = raw
