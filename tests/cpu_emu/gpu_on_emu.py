@@ -7,11 +7,13 @@ through tests/conftest.py, e.g.
 The emulated library (tests/cpu_emu/build.py) takes host pointers, so CPU
 tensors stand in for device tensors:
   * a TorchFunctionMode maps every device="cuda" argument (factories,
-    Tensor.to, Tensor.cuda) to the CPU, and pin_memory to a no-op;
+    Tensor.to, Tensor.cuda) to the CPU, an upload to a copy, and pin_memory
+    to a no-op;
   * every tensor reports is_cuda, so the package takes its device path;
   * torch.cuda's synchronisation, streams, device and memory queries become
-    host no-ops; HIP-graph capture is not emulated, so a test that captures
-    one is skipped at that point;
+    host no-ops (a 4 GiB device, which bounds the engine's KV cache);
+    HIP-graph capture is not emulated, so a test that captures one is
+    skipped at that point;
   * nanovllm.quantization._hip loads the emulated library, with a 256-byte
     aligned workspace.
 The tests' own checks then run unchanged against the kernels' emulation.
@@ -36,14 +38,20 @@ def _is_cuda(d) -> bool:
 class _CudaAsCpu(TorchFunctionMode):
     def __torch_function__(self, func, types_, args=(), kwargs=None):
         kwargs = dict(kwargs or {})
-        if func is torch.Tensor.cuda or func is torch.Tensor.pin_memory:
+        if func is torch.Tensor.pin_memory:
             return args[0]
-        if _is_cuda(kwargs.get("device")):
+        if func is torch.Tensor.cuda:
+            return args[0].clone()  # an upload is a copy (callers may update the host tensor afterwards)
+        upload = _is_cuda(kwargs.get("device"))
+        if upload:
             kwargs["device"] = "cpu"
         if kwargs.get("pin_memory"):
             kwargs["pin_memory"] = False
         if func is torch.Tensor.to:
+            upload = upload or any(_is_cuda(a) for a in args)
             args = tuple("cpu" if _is_cuda(a) else a for a in args)
+            out = func(*args, **kwargs)
+            return out.clone() if upload and out is args[0] else out
         return func(*args, **kwargs)
 
 
@@ -100,8 +108,9 @@ def install(lib) -> None:
     c.CUDAGraph = _no_graphs
     c.graph = _no_graphs
     c.empty_cache = lambda: None
-    c.mem_get_info = lambda *a: (256 << 30, 288 << 30)
-    c.memory_stats = lambda *a: {}
+    # a 4 GiB "device", so that the engine sizes its KV cache within host memory
+    c.mem_get_info = lambda *a: (4 << 30, 4 << 30)
+    c.memory_stats = lambda *a: {"allocated_bytes.all.current": 0}
     c.reset_peak_memory_stats = lambda *a: None
     c.max_memory_allocated = lambda *a: 0
     c.manual_seed = lambda *a: None
