@@ -16,7 +16,7 @@ from safetensors.torch import save_file
 from nanovllm import LLM, SamplingParams
 from nanovllm.engine.model_runner import random_init_
 from nanovllm.engine.scheduler import Scheduler
-from nanovllm.engine.sequence import Sequence, SequenceStatus
+from nanovllm.engine.sequence import Sequence
 from nanovllm.models.qwen3 import Qwen3Config
 from nanovllm.utils.context import step_context
 
