@@ -12,10 +12,16 @@ tensors stand in for device tensors:
   * every tensor reports is_cuda, so the package takes its device path;
   * torch.cuda's synchronisation, streams, device and memory queries become
     host no-ops (a 4 GiB device, which bounds the engine's KV cache);
-    HIP-graph capture is not emulated, so a test that captures one is
-    skipped at that point;
   * nanovllm.quantization._hip loads the emulated library, with a 256-byte
-    aligned workspace.
+    aligned workspace;
+  * HIP graphs: capture runs its code eagerly and records, in order, every
+    top-level torch call and every library call; replay runs them again,
+    copying each out-of-place torch result into the tensor the capture
+    produced (so the later calls, which hold its address, see the new
+    values), as a replayed graph rewrites its buffers in place. This checks
+    what a graph's users must get right (static inputs filled before
+    replay, outputs read after it, nothing allocated while capturing); it
+    does not model the GPU's graph nodes themselves.
 The tests' own checks then run unchanged against the kernels' emulation.
 Random data differ from a GPU run (CPU generators), and nothing is timed.
 """
@@ -24,9 +30,19 @@ from __future__ import annotations
 import contextlib
 import types
 
-import pytest
 import torch
 from torch.overrides import TorchFunctionMode
+
+
+_CAPTURE = None  # the graph being captured
+
+
+def _record(kind, fn, args, kwargs=None, out=None) -> None:
+    if _CAPTURE is not None:
+        _CAPTURE.ops.append((kind, fn, args, kwargs or {}, out))
+
+
+_NO_REPLAY = {torch.empty, torch.empty_like, torch.Tensor.new_empty}
 
 
 def _is_cuda(d) -> bool:
@@ -51,8 +67,16 @@ class _CudaAsCpu(TorchFunctionMode):
             upload = upload or any(_is_cuda(a) for a in args)
             args = tuple("cpu" if _is_cuda(a) else a for a in args)
             out = func(*args, **kwargs)
-            return out.clone() if upload and out is args[0] else out
-        return func(*args, **kwargs)
+            out = out.clone() if upload and out is args[0] else out
+        else:
+            out = func(*args, **kwargs)
+        if _CAPTURE is not None:
+            if func in _NO_REPLAY:
+                _CAPTURE.keep.append(out)  # the graph's pool owns what its capture allocates
+            elif out is None or isinstance(out, torch.Tensor) or (
+                    isinstance(out, tuple) and out and all(isinstance(o, torch.Tensor) for o in out)):
+                _record("torch", func, args, kwargs, out)
+        return out
 
 
 class _Stream:
@@ -71,8 +95,58 @@ class _Stream:
         return None
 
 
-def _no_graphs(*a, **k):
-    pytest.skip("HIP-graph capture is not emulated")
+class _Graph:
+    """torch.cuda.CUDAGraph on the emulation (see the module docstring)."""
+
+    def __init__(self, *a, **k):
+        self.ops = []
+        self.keep = []  # tensors allocated during capture (held like the graph's memory pool)
+
+    def replay(self) -> None:
+        global _CAPTURE
+        assert _CAPTURE is None, "replay while capturing"
+        for kind, fn, args, kwargs, out in self.ops:
+            new = fn(*args, **kwargs)
+            if kind == "torch":
+                outs, news = (out, new) if isinstance(out, tuple) else ((out,), (new,))
+                for o, n in zip(outs, news):
+                    if isinstance(o, torch.Tensor) and n is not o:
+                        o.copy_(n)
+
+    def pool(self):
+        return None
+
+    def reset(self) -> None:
+        self.ops, self.keep = [], []
+
+
+@contextlib.contextmanager
+def _graph(g, pool=None, stream=None, **kw):
+    global _CAPTURE
+    assert _CAPTURE is None, "nested capture"
+    _CAPTURE = g
+    try:
+        yield g
+    finally:
+        _CAPTURE = None
+
+
+class _Lib:
+    """The emulated library, each call also recorded while a graph captures."""
+
+    def __init__(self, lib):
+        self._lib = lib
+
+    def __getattr__(self, name):
+        fn = getattr(self._lib, name)
+        if not callable(fn):
+            return fn
+
+        def call(*args):
+            r = fn(*args)
+            _record("lib", fn, args)
+            return r
+        return call
 
 
 _GENERATOR = torch.Generator
@@ -104,9 +178,10 @@ def install(lib) -> None:
     c.default_stream = lambda *a, **k: _Stream()
     c.Stream = _Stream
     c.stream = lambda *a, **k: contextlib.nullcontext()
-    c.is_current_stream_capturing = lambda: False
-    c.CUDAGraph = _no_graphs
-    c.graph = _no_graphs
+    c.is_current_stream_capturing = lambda: _CAPTURE is not None
+    c.CUDAGraph = _Graph
+    c.graph = _graph
+    c.graph_pool_handle = lambda: None
     c.empty_cache = lambda: None
     # a 4 GiB "device", so that the engine sizes its KV cache within host memory
     c.mem_get_info = lambda *a: (4 << 30, 4 << 30)
@@ -124,7 +199,8 @@ def install(lib) -> None:
     raw = torch.zeros(n + 256, dtype=torch.uint8)
     off = (-raw.data_ptr()) % 256
     ws = raw[off:off + n]
-    _hip.load_library = lambda: lib
+    proxy = _Lib(lib)
+    _hip.load_library = lambda: proxy
     _hip._stream = lambda dev: None
     _hip.gemm_workspace = lambda dev: ws
     _hip._emu_keep = raw
