@@ -131,6 +131,23 @@ def _graph(g, pool=None, stream=None, **kw):
         _CAPTURE = None
 
 
+class _Event:
+    """torch.cuda.Event on the host clock (emulated kernels run synchronously)."""
+
+    def __init__(self, *a, **k):
+        self.t = None
+
+    def record(self, *a):
+        import time
+        self.t = time.perf_counter()
+
+    def synchronize(self):
+        pass
+
+    def elapsed_time(self, end) -> float:
+        return (end.t - self.t) * 1e3
+
+
 class _Lib:
     """The emulated library, each call also recorded while a graph captures."""
 
@@ -182,6 +199,7 @@ def install(lib) -> None:
     c.CUDAGraph = _Graph
     c.graph = _graph
     c.graph_pool_handle = lambda: None
+    c.Event = _Event
     c.empty_cache = lambda: None
     # a 4 GiB "device", so that the engine sizes its KV cache within host memory
     c.mem_get_info = lambda *a: (4 << 30, 4 << 30)
