@@ -31,9 +31,12 @@ from nanovllm.models.qwen3 import Qwen3Config
 
 
 def make_workload(num_seqs: int, max_input_len: int, max_output_len: int, seed: int):
+    # lengths uniform in [100, max], the reference benchmark's workload (the
+    # lower bound shrinks with a smaller max, for short runs)
     rng = random.Random(seed)
-    prompts = [[rng.randint(0, 10000) for _ in range(rng.randint(100, max_input_len))] for _ in range(num_seqs)]
-    params = [SamplingParams(temperature=0.0, ignore_eos=True, max_tokens=rng.randint(100, max_output_len))
+    lo_in, lo_out = min(100, max_input_len), min(100, max_output_len)
+    prompts = [[rng.randint(0, 10000) for _ in range(rng.randint(lo_in, max_input_len))] for _ in range(num_seqs)]
+    params = [SamplingParams(temperature=0.0, ignore_eos=True, max_tokens=rng.randint(lo_out, max_output_len))
               for _ in range(num_seqs)]
     return prompts, params
 
