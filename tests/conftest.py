@@ -20,13 +20,24 @@ def pytest_configure(config):
 
 
 # TVQ_GPU_TESTS_ON_EMU=1: the -m gpu tests run on the CPU emulation of the
-# kernels (tests/cpu_emu/gpu_on_emu.py), CPU tensors standing in for device ones.
+# kernels (tests/cpu_emu/gpu_on_emu.py), CPU tensors standing in for device
+# ones; with TVQ_EMU_RACE=1 (and EMU_DMA=late) on its race-checking build,
+# each test failing if it adds a race report.
 ON_EMU = os.environ.get("TVQ_GPU_TESTS_ON_EMU") == "1"
+EMU_RACE = ON_EMU and os.environ.get("TVQ_EMU_RACE") == "1"
 if ON_EMU:
     sys.path.insert(0, str(ROOT / "tests" / "cpu_emu"))
     import emu
     import gpu_on_emu
-    gpu_on_emu.install(emu.load())
+    _EMU_LIB = emu.load(race=EMU_RACE)
+    gpu_on_emu.install(_EMU_LIB)
+
+    @pytest.fixture(autouse=True)
+    def _emu_race_reports():
+        before = _EMU_LIB.tvq_emu_race_reports() if EMU_RACE else 0
+        yield
+        if EMU_RACE:
+            assert _EMU_LIB.tvq_emu_race_reports() == before, "race report(s) on stderr"
 
 
 @pytest.fixture(scope="session")
